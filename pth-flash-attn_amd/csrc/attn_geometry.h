@@ -1,0 +1,212 @@
+// attn_geometry.h -- integer geometry of one attention launch, shared by the
+// gfx950 kernels and the host launcher (and compiled by g++ for the CPU
+// tests through geometry_capi.cpp).
+//
+// It answers, with integer arithmetic only:
+//   * division by run-time divisors (block size, GQA group, row-tile height)
+//     as one multiply-high and a shift;
+//   * which request and query tokens a row tile x owns (the q-tile numbering
+//     of vLLM's unified attention, reference cache_geometry.cuh:336-394);
+//   * the visible key range [lo, hi] of a query token (causal, sliding
+//     window, non-causal; reference cache_geometry.cuh:396-468);
+//   * the KV tiles of a row tile and how they are cut into splits
+//     (reference cache_geometry.cuh:426-432, 506-515), with the MI355X
+//     addition that a row tile uses only as many splits as its length needs
+//     (live_splits below).
+// Header-only; needs <stdint.h> only.
+
+#pragma once
+
+#include <stdint.h>
+
+#if defined(__HIPCC__)
+#define PA_HD __host__ __device__ __forceinline__
+#else
+#define PA_HD inline
+#endif
+
+namespace pa {
+
+// KV tokens per tile: the unit of the split partition (the planner's
+// KV_TILE_TOKENS; reference tile_traits.cuh / planner.py:98).
+constexpr int32_t kTileTokens = 64;
+// KV tokens per softmax step of one wave (two 16-token MFMA column blocks).
+constexpr int32_t kChunkTokens = 32;
+// Query rows per wave: the N of a 16x16x32 MFMA.
+constexpr int32_t kRowsPerWave = 16;
+// Waves per workgroup.
+constexpr int32_t kWaves = 4;
+// A row tile uses no more splits than ceil(tiles / kMinTilesPerSplit): a
+// split shorter than this costs more in prologue and combine than it gains
+// in parallelism. The extra splits of the grid exit at once with lse = -inf.
+constexpr int32_t kMinTilesPerSplit = 4;
+
+PA_HD uint32_t mulhi32(uint32_t a, uint32_t b) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  return __umulhi(a, b);
+#else
+  return static_cast<uint32_t>((static_cast<uint64_t>(a) * b) >> 32);
+#endif
+}
+
+// Exact n / d for 0 <= n < 2^31 and 1 <= d < 2^31.
+// Construction: s = ceil(log2 d), p = 31 + s, m = ceil(2^p / d) (< 2^32).
+// With m d = 2^p + e, 0 <= e < d <= 2^s, n m / 2^p = n / d + n e / (d 2^p)
+// and n e < 2^31 2^s = 2^p, so the error term is below 1/d and the floor
+// is exact (Granlund & Montgomery, PLDI 1994, Thm 4.2). d = 1 is the
+// identity (mul = 0 marks it).
+struct Div32 {
+  uint32_t d;
+  uint32_t mul;
+  uint32_t shift;  // p - 32 = s - 1
+
+  static Div32 make(uint32_t dv) {
+    Div32 r{dv, 0u, 0u};
+    if (dv <= 1u) return r;
+    uint32_t s = 0;
+    while ((uint64_t{1} << s) < dv) ++s;
+    const uint64_t two_p = uint64_t{1} << (31 + s);
+    r.mul = static_cast<uint32_t>((two_p + dv - 1) / dv);
+    r.shift = s - 1;
+    return r;
+  }
+  PA_HD uint32_t div(uint32_t n) const {
+    return mul == 0u ? n : (mulhi32(n, mul) >> shift);
+  }
+};
+
+// One row tile of query tokens of one request.
+struct RowTile {
+  int32_t req;        // request index
+  int32_t tok_begin;  // first query token of the tile within the request
+  int32_t num_tok;    // query tokens in the tile (1..bq)
+  int32_t q_len;      // query tokens of the request
+  int32_t seq_len;    // KV length of the request, new tokens included
+  int32_t q_start;    // global index of the request's first query token
+};
+
+// Request r owns the tile indices [qsl[r] / bq + r, qsl[r+1] / bq + r + 1):
+// at least ceil(q_len / bq) tiles, and the last request ends at or below
+// T / bq + R, the planner's q_tiles_upper (reference cache_geometry.cuh:336-350).
+PA_HD int32_t first_tile_of(const int32_t* qsl, const Div32& bq, int32_t r) {
+  return static_cast<int32_t>(bq.div(static_cast<uint32_t>(qsl[r]))) + r;
+}
+
+// Largest r in [0, R) with first_tile_of(r) <= x (strictly increasing in r).
+PA_HD int32_t request_of_tile(const int32_t* qsl, const Div32& bq, int32_t R,
+                              int32_t x) {
+  int32_t lo = 0, hi = R - 1;
+  while (lo < hi) {
+    const int32_t mid = (lo + hi + 1) >> 1;
+    if (first_tile_of(qsl, bq, mid) <= x) lo = mid; else hi = mid - 1;
+  }
+  return lo;
+}
+
+// Fills t for row tile x; false when the tile holds no query token.
+PA_HD bool row_tile(const int32_t* qsl, const int32_t* seq_lens,
+                    const Div32& bq, int32_t R, int32_t x, RowTile& t) {
+  if (R <= 0) return false;
+  const int32_t r = request_of_tile(qsl, bq, R, x);
+  t.req = r;
+  t.q_start = qsl[r];
+  t.q_len = qsl[r + 1] - t.q_start;
+  t.seq_len = seq_lens[r];
+  const int64_t begin =
+      static_cast<int64_t>(x - first_tile_of(qsl, bq, r)) * static_cast<int64_t>(bq.d);
+  if (begin >= t.q_len) return false;
+  t.tok_begin = static_cast<int32_t>(begin);
+  const int32_t left = t.q_len - t.tok_begin;
+  t.num_tok = left < static_cast<int32_t>(bq.d) ? left : static_cast<int32_t>(bq.d);
+  return true;
+}
+
+// Absolute KV position of query token `tok` of the request (bottom-right).
+PA_HD int32_t query_pos(const RowTile& t, int32_t tok) {
+  return t.seq_len - t.q_len + tok;
+}
+
+// Inclusive visible key range of query token `tok` (reference
+// reference.py:553-593 visible_mask / visible_bounds).
+PA_HD int32_t key_lo(const RowTile& t, int32_t tok, int32_t window) {
+  const int32_t p = query_pos(t, tok);
+  return (window > 0 && p >= window) ? p - window + 1 : 0;
+}
+PA_HD int32_t key_hi(const RowTile& t, int32_t tok, int32_t window,
+                     bool causal) {
+  const int32_t p = query_pos(t, tok);
+  if (causal) return p;
+  return (window > 0 && t.seq_len - 1 - p >= window) ? p + window - 1
+                                                     : t.seq_len - 1;
+}
+
+// The keys any token of the tile sees: [range_begin, range_end). Both bounds
+// are non-decreasing in the token, so they come from the first and the last
+// token of the tile.
+PA_HD int32_t range_begin(const RowTile& t, int32_t window) {
+  return key_lo(t, t.tok_begin, window);
+}
+PA_HD int32_t range_end(const RowTile& t, int32_t window, bool causal) {
+  return key_hi(t, t.tok_begin + t.num_tok - 1, window, causal) + 1;
+}
+
+// KV tiles of the row tile: [first, first + count).
+PA_HD int32_t first_kv_tile(int32_t rbegin) { return rbegin / kTileTokens; }
+PA_HD int32_t kv_tile_count(int32_t rbegin, int32_t rend) {
+  return (rend + kTileTokens - 1) / kTileTokens - first_kv_tile(rbegin);
+}
+
+// Splits a row tile with `count` KV tiles actually uses, out of the grid's
+// num_splits: never more than count / kMinTilesPerSplit (rounded up), never
+// fewer than 1. Read on the device from the device-side lengths, so a
+// captured graph stays valid for any length.
+PA_HD int32_t live_splits(int32_t count, int32_t num_splits) {
+  int32_t want = (count + kMinTilesPerSplit - 1) / kMinTilesPerSplit;
+  if (want < 1) want = 1;
+  return want < num_splits ? want : num_splits;
+}
+
+// Row tile j (0-based) of a request: query tokens [j bq, min((j + 1) bq, q_len)).
+PA_HD RowTile request_tile(int32_t req, int32_t q_start, int32_t q_len,
+                           int32_t seq_len, int32_t bq, int32_t j) {
+  RowTile t;
+  t.req = req;
+  t.q_start = q_start;
+  t.q_len = q_len;
+  t.seq_len = seq_len;
+  t.tok_begin = j * bq;
+  const int32_t left = q_len - t.tok_begin;
+  t.num_tok = left < bq ? left : bq;
+  return t;
+}
+
+// Row tiles of a request: ceil(q_len / bq).
+PA_HD int32_t request_row_tiles(int32_t q_len, int32_t bq) {
+  return (q_len + bq - 1) / bq;
+}
+
+// Splits every row tile of a request uses: the live split count of its last
+// row tile, whose key range is the widest (it ends at seq_len; with a window
+// every tile sees about the same number of keys). One count per request keeps
+// the device-side work table a prefix sum over requests.
+PA_HD int32_t request_splits(int32_t q_len, int32_t seq_len, int32_t bq,
+                             int32_t window, bool causal, int32_t num_splits) {
+  if (q_len <= 0) return 0;
+  const RowTile t = request_tile(0, 0, q_len, seq_len, bq,
+                                 request_row_tiles(q_len, bq) - 1);
+  const int32_t rb = window > 0 ? range_begin(t, window) : 0;
+  const int32_t re = range_end(t, window, causal);
+  return live_splits(kv_tile_count(rb, re), num_splits);
+}
+
+// Tiles [begin, end) (relative to the first tile) of split s < live:
+// [floor(s n / live), floor((s + 1) n / live)); any two differ by at most one
+// tile and they partition [0, n) (reference cache_geometry.cuh:426-432 with
+// the live split count in place of the grid's).
+PA_HD void split_range(int32_t s, int32_t live, int32_t count, int32_t& begin,
+                       int32_t& end) {
+  begin = static_cast<int32_t>(static_cast<int64_t>(s) * count / live);
+  end = static_cast<int32_t>(static_cast<int64_t>(s + 1) * count / live);
+}
+
+}  // namespace pa

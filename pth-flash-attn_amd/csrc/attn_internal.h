@@ -1,0 +1,107 @@
+// attn_internal.h -- device-side launch parameters and the host launchers of
+// libpth_attn.so (not part of the C ABI; include/pth_attn.h is).
+
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "attn_geometry.h"
+#include "pth_attn.h"
+
+namespace pa {
+
+// One cache stream as the kernels read it: byte strides of [NB, BS, Hkv].
+struct CacheStream {
+  const char* base;
+  int64_t s_block;
+  int64_t s_slot;
+  int64_t s_head;
+};
+
+// Everything one attention launch reads; passed by value as the kernel
+// argument. Built by launch_attention from PthAttnArgs.
+struct AttnParams {
+  const char* q;
+  int64_t s_q_tok, s_q_head;
+  char* out;
+  int64_t s_out_tok, s_out_head;
+  float* ws_o;
+  int64_t s_wo_split, s_wo_tok, s_wo_head;
+  float* ws_lse;
+  int64_t s_wl_split, s_wl_tok, s_wl_head;
+  float* lse_out;  // optional natural-log LSE of every row (S == 1 only)
+  int64_t s_lo_tok, s_lo_head;
+  CacheStream k, v, ks, vs;
+  const int32_t* block_table;
+  int64_t bt_stride;  // elements
+  const int32_t* seq_lens;
+  const int32_t* qsl;
+  Div32 bs_div;  // block size
+  Div32 g_div;   // GQA group
+  Div32 bq_div;  // query tokens per row tile
+  Div32 rg_div;  // 16-row groups per row tile
+  int32_t num_reqs;
+  int32_t n_hu;  // work units per (row tile, split): num_kv_heads * row groups
+  int32_t bq;    // query tokens per row tile
+  int32_t group;
+  int32_t num_splits;
+  int32_t window;
+  int32_t causal;
+  int32_t out_dtype;
+  float scale_log2;  // softmax_scale * log2(e)
+};
+
+struct CombineParams {
+  const char* ws_o;
+  int64_t s_wo_split, s_wo_tok, s_wo_head;
+  const char* ws_lse;
+  int64_t s_wl_split, s_wl_tok, s_wl_head;
+  char* out;
+  int64_t s_out_tok, s_out_head;
+  int32_t out_dtype;
+  float* lse_out;  // optional natural-log LSE
+  int64_t s_lo_tok, s_lo_head;
+  const int32_t* qsl;
+  int32_t num_reqs;
+  int32_t num_tokens;
+  int32_t num_q_heads;
+  int32_t num_splits;
+  // When seq_lens is non-NULL the combine reads only the splits the
+  // attention kernel used for the row's request (request_splits with these
+  // bq / window / causal); otherwise all num_splits.
+  const int32_t* seq_lens;
+  int32_t bq;
+  int32_t window;
+  int32_t causal;
+};
+
+// Host launchers. They check their arguments, enqueue on `stream`, allocate
+// nothing and never synchronise. Return PTH_ATTN_OK, EINVAL or ECUDA; the
+// message of a failure is last_error() on the calling thread.
+int32_t launch_attention(const PthAttnArgs& a, int32_t loader,
+                         hipStream_t stream, float* lse_out,
+                         int64_t lse_stride_token, int64_t lse_stride_head);
+int32_t launch_combine(const PthAttnCombineArgs& c, hipStream_t stream,
+                       float* lse_out, int64_t lse_stride_token,
+                       int64_t lse_stride_head, const PthAttnArgs* split_source);
+
+// Per-variant kernel launches (attn_fwd.hip, attn_combine.hip).
+// Work-groups of kWaves waves that fill the device once (CUs x 2).
+int32_t resident_workgroups();
+hipError_t launch_fwd_kernel(const AttnParams& p, dim3 grid, bool windowed,
+                             bool paged16, bool q_f16, hipStream_t stream);
+hipError_t launch_combine_kernel(const CombineParams& c, hipStream_t stream);
+
+const char* last_error();
+int32_t fail(int32_t code, const std::string& msg);
+void clear_error();
+
+}  // namespace pa
+
+#define PA_REQUIRE(cond, msg)                                   \
+  do {                                                          \
+    if (!(cond)) return ::pa::fail(PTH_ATTN_EINVAL, (msg));     \
+  } while (0)

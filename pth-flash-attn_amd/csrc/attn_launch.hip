@@ -1,0 +1,379 @@
+// attn_launch.hip -- host launchers (argument checks, parameter packing,
+// variant dispatch) and the C ABI of include/pth_attn.h.
+//
+// Responsibilities follow the reference launcher (attn_launch.cu:63-236,
+// attn_combine.cu:356-411, attn_capi.cu): every check names the field, the
+// byte strides are copied as given, nothing is allocated, nothing is read
+// back and nothing synchronises. The torch op (torch_op.cpp) and the C ABI
+// both launch through launch_attention / launch_combine, so the op runs
+// exactly the code the C-ABI tests exercise.
+
+#include <cmath>
+#include <string>
+
+#include "attn_internal.h"
+
+namespace pa {
+namespace {
+
+thread_local std::string g_last_error;
+
+constexpr float kLog2e = 1.44269504088896340736f;
+constexpr int64_t kVecAlign = 16;
+
+bool aligned(const void* ptr, int64_t a) {
+  return reinterpret_cast<uintptr_t>(ptr) % static_cast<uintptr_t>(a) == 0;
+}
+
+// A cache stream needs 4-byte alignment of its base and of every byte stride
+// that multiplies a non-zero index (a size-1 dimension's stride never reaches
+// an address). Reference cache_geometry.cuh:200-222 (the 4-byte floor).
+bool stream_aligned(const PthAttnStream& s, const PthAttnArgs& a) {
+  if (!aligned(s.data, 4)) return false;
+  if (a.num_blocks > 1 && s.stride_block % 4 != 0) return false;
+  if (a.block_size > 1 && s.stride_slot % 4 != 0) return false;
+  if (a.num_kv_heads > 1 && s.stride_head % 4 != 0) return false;
+  return true;
+}
+
+CacheStream cache_stream(const PthAttnStream& s) {
+  return CacheStream{static_cast<const char*>(s.data), s.stride_block,
+                     s.stride_slot, s.stride_head};
+}
+
+}  // namespace
+
+int32_t resident_workgroups() {
+  // 8 waves per CU (2 per SIMD at <= 256 VGPRs) = 2 work-groups of kWaves.
+  constexpr int kMaxDevices = 64;
+  static int32_t cached[kMaxDevices] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 0;
+  if (dev < kMaxDevices && cached[dev] > 0) return cached[dev];
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      cus <= 0)
+    return 0;
+  const int32_t wgs = cus * 2;
+  if (dev < kMaxDevices) cached[dev] = wgs;
+  return wgs;
+}
+
+const char* last_error() { return g_last_error.c_str(); }
+int32_t fail(int32_t code, const std::string& msg) {
+  g_last_error = msg;
+  return code;
+}
+void clear_error() { g_last_error.clear(); }
+
+int32_t launch_attention(const PthAttnArgs& a, int32_t loader,
+                         hipStream_t stream, float* lse_out,
+                         int64_t lse_stride_token, int64_t lse_stride_head) {
+  clear_error();
+  PA_REQUIRE(loader >= 0 && loader <= 2,
+             "options.loader must be 0 (default), 1 (separate) or 2 (cell)");
+  PA_REQUIRE(loader != 2,
+             "options.loader = cell: the whole-cell loader is not built in "
+             "this library (its kernels read the four streams separately)");
+  PA_REQUIRE(a.q_dtype == PTH_ATTN_F16 || a.q_dtype == PTH_ATTN_BF16,
+             "q_dtype must be PTH_ATTN_F16 or PTH_ATTN_BF16");
+  PA_REQUIRE(a.out_dtype == PTH_ATTN_F32 || a.out_dtype == PTH_ATTN_F16 ||
+                 a.out_dtype == PTH_ATTN_BF16,
+             "out_dtype must be PTH_ATTN_F32, PTH_ATTN_F16 or PTH_ATTN_BF16");
+  PA_REQUIRE(a.head_size == 64 || a.head_size == 128 || a.head_size == 256,
+             "head_size must be 64, 128 or 256");
+  PA_REQUIRE(a.head_size == 128,
+             "head_size " + std::to_string(a.head_size) +
+                 " has no gfx950 kernel in this library (D = 128 only)");
+  PA_REQUIRE(a.num_kv_heads >= 1 && a.num_q_heads >= a.num_kv_heads &&
+                 a.num_q_heads % a.num_kv_heads == 0,
+             "num_q_heads must be a positive multiple of num_kv_heads");
+  PA_REQUIRE(a.block_size >= 1, "block_size must be >= 1");
+  PA_REQUIRE(a.num_blocks >= 1, "num_blocks must be >= 1");
+  PA_REQUIRE(a.num_reqs >= 1, "num_reqs must be >= 1");
+  PA_REQUIRE(a.num_tokens >= 1, "num_tokens must be >= 1");
+  PA_REQUIRE(a.bq >= 1, "bq must be >= 1");
+  PA_REQUIRE(a.num_splits >= 1, "num_splits must be >= 1");
+  PA_REQUIRE(a.num_splits <= 65535, "num_splits must be <= 65535 (grid z)");
+  PA_REQUIRE(a.num_q_tiles >= 0, "num_q_tiles must be >= 0");
+  PA_REQUIRE(std::isfinite(a.softmax_scale) && a.softmax_scale > 0.0f,
+             "softmax_scale must be finite and > 0");
+  PA_REQUIRE(a.window >= 0, "window must be >= 0 (0 = none)");
+  PA_REQUIRE(a.causal == 0 || a.causal == 1, "causal must be 0 or 1");
+  PA_REQUIRE(a.q && a.k_cache.data && a.v_cache.data && a.k_scale.data &&
+                 a.v_scale.data && a.block_table && a.seq_lens &&
+                 a.query_start_loc,
+             "q, the four cache streams, block_table, seq_lens and "
+             "query_start_loc must be non-NULL");
+  const int32_t group = a.num_q_heads / a.num_kv_heads;
+  const int64_t rows = static_cast<int64_t>(a.bq) * group;
+  PA_REQUIRE(rows <= 64, "bq * G = " + std::to_string(rows) +
+                             " rows exceed one 64-row tile");
+  PA_REQUIRE(aligned(a.q, kVecAlign) && a.q_stride_token % kVecAlign == 0 &&
+                 a.q_stride_head % kVecAlign == 0,
+             "q base and byte strides must be 16-B aligned");
+  if (a.num_splits == 1) {
+    PA_REQUIRE(a.out != nullptr, "out must be non-NULL when num_splits == 1");
+    PA_REQUIRE(aligned(a.out, kVecAlign) &&
+                   a.out_stride_token % kVecAlign == 0 &&
+                   a.out_stride_head % kVecAlign == 0,
+               "out base and byte strides must be 16-B aligned");
+  } else {
+    PA_REQUIRE(a.ws_o != nullptr && a.ws_lse != nullptr,
+               "ws_o and ws_lse must be non-NULL when num_splits > 1");
+    PA_REQUIRE(aligned(a.ws_o, kVecAlign) &&
+                   a.ws_o_stride_split % kVecAlign == 0 &&
+                   a.ws_o_stride_token % kVecAlign == 0 &&
+                   a.ws_o_stride_head % kVecAlign == 0,
+               "ws_o base and byte strides must be 16-B aligned");
+    PA_REQUIRE(aligned(a.ws_lse, 4) && a.ws_lse_stride_split % 4 == 0 &&
+                   a.ws_lse_stride_token % 4 == 0 &&
+                   a.ws_lse_stride_head % 4 == 0,
+               "ws_lse base and byte strides must be 4-B aligned");
+  }
+  const PthAttnStream* streams[4] = {&a.k_cache, &a.v_cache, &a.k_scale,
+                                     &a.v_scale};
+  for (int i = 0; i < 4; ++i) {
+    PA_REQUIRE(stream_aligned(*streams[i], a),
+               "cache stream " + std::to_string(i) +
+                   " (K, V, k_scale, v_scale) is not 4-B aligned");
+  }
+
+  const int32_t n_rg = static_cast<int32_t>((rows + kRowsPerWave - 1) / kRowsPerWave);
+  AttnParams p{};
+  p.q = static_cast<const char*>(a.q);
+  p.s_q_tok = a.q_stride_token;
+  p.s_q_head = a.q_stride_head;
+  p.out = static_cast<char*>(a.out);
+  p.s_out_tok = a.out_stride_token;
+  p.s_out_head = a.out_stride_head;
+  p.ws_o = a.ws_o;
+  p.s_wo_split = a.ws_o_stride_split;
+  p.s_wo_tok = a.ws_o_stride_token;
+  p.s_wo_head = a.ws_o_stride_head;
+  p.ws_lse = a.ws_lse;
+  p.s_wl_split = a.ws_lse_stride_split;
+  p.s_wl_tok = a.ws_lse_stride_token;
+  p.s_wl_head = a.ws_lse_stride_head;
+  p.lse_out = a.num_splits == 1 ? lse_out : nullptr;
+  p.s_lo_tok = lse_stride_token;
+  p.s_lo_head = lse_stride_head;
+  p.k = cache_stream(a.k_cache);
+  p.v = cache_stream(a.v_cache);
+  p.ks = cache_stream(a.k_scale);
+  p.vs = cache_stream(a.v_scale);
+  p.block_table = a.block_table;
+  p.bt_stride = a.block_table_row_stride;
+  p.seq_lens = a.seq_lens;
+  p.qsl = a.query_start_loc;
+  p.bs_div = Div32::make(static_cast<uint32_t>(a.block_size));
+  p.g_div = Div32::make(static_cast<uint32_t>(group));
+  p.bq_div = Div32::make(static_cast<uint32_t>(a.bq));
+  p.rg_div = Div32::make(static_cast<uint32_t>(n_rg));
+  p.num_reqs = a.num_reqs;
+  p.n_hu = a.num_kv_heads * n_rg;
+  p.bq = a.bq;
+  p.group = group;
+  p.num_splits = a.num_splits;
+  p.window = a.window;
+  p.causal = a.causal;
+  p.out_dtype = a.out_dtype;
+  p.scale_log2 = a.softmax_scale * kLog2e;
+
+  // Persistent grid: one wave per resident slot, but never more waves than
+  // the unit table can hold (sum over requests of row tiles x S x units is
+  // at most (T / bq + R) x S x n_hu).
+  const int64_t tile_bound =
+      a.num_q_tiles > 0 ? a.num_q_tiles
+                        : static_cast<int64_t>(a.num_tokens) / a.bq + a.num_reqs;
+  const int64_t unit_bound = tile_bound * a.num_splits * p.n_hu;
+  const int64_t wg_need = (unit_bound + kWaves - 1) / kWaves;
+  const int32_t wg_fill = resident_workgroups();
+  PA_REQUIRE(wg_fill > 0, "cannot query the compute-unit count of the current device");
+  PA_REQUIRE(unit_bound < 0x7fffffff, "the work table exceeds 2^31 - 1 units");
+  const dim3 grid(static_cast<unsigned>(wg_need < wg_fill ? wg_need : wg_fill));
+  const bool windowed = a.window > 0 || a.causal == 0;
+  const bool paged16 = a.block_size % 16 == 0;
+  const hipError_t err = launch_fwd_kernel(p, grid, windowed, paged16,
+                                           a.q_dtype == PTH_ATTN_F16, stream);
+  if (err != hipSuccess) {
+    return fail(PTH_ATTN_ECUDA, std::string("attention launch (D=128, rows=") +
+                                    std::to_string(rows) + "): " +
+                                    hipGetErrorString(err));
+  }
+  return PTH_ATTN_OK;
+}
+
+int32_t launch_combine(const PthAttnCombineArgs& c, hipStream_t stream,
+                       float* lse_out, int64_t lse_stride_token,
+                       int64_t lse_stride_head, const PthAttnArgs* split_source) {
+  clear_error();
+  PA_REQUIRE(c.head_size == 128,
+             "head_size " + std::to_string(c.head_size) +
+                 " has no gfx950 combine in this library (D = 128 only)");
+  PA_REQUIRE(c.out_dtype == PTH_ATTN_F32 || c.out_dtype == PTH_ATTN_F16 ||
+                 c.out_dtype == PTH_ATTN_BF16,
+             "out_dtype must be PTH_ATTN_F32, PTH_ATTN_F16 or PTH_ATTN_BF16");
+  PA_REQUIRE(c.num_splits >= 1, "num_splits must be >= 1");
+  PA_REQUIRE(c.num_reqs >= 1, "num_reqs must be >= 1");
+  PA_REQUIRE(c.num_tokens >= 1, "num_tokens must be >= 1");
+  PA_REQUIRE(c.num_q_heads >= 1, "num_q_heads must be >= 1");
+  PA_REQUIRE(c.ws_o && c.ws_lse && c.out && c.query_start_loc,
+             "ws_o, ws_lse, out and query_start_loc must be non-NULL");
+  PA_REQUIRE(aligned(c.ws_o, 8) && c.ws_o_stride_split % 8 == 0 &&
+                 c.ws_o_stride_token % 8 == 0 && c.ws_o_stride_head % 8 == 0,
+             "ws_o base and byte strides must be 8-B aligned");
+  PA_REQUIRE(aligned(c.ws_lse, 4) && c.ws_lse_stride_split % 4 == 0 &&
+                 c.ws_lse_stride_token % 4 == 0 &&
+                 c.ws_lse_stride_head % 4 == 0,
+             "ws_lse base and byte strides must be 4-B aligned");
+  const int64_t elem = c.out_dtype == PTH_ATTN_F32 ? 8 : 4;
+  PA_REQUIRE(aligned(c.out, elem) && c.out_stride_token % elem == 0 &&
+                 c.out_stride_head % elem == 0,
+             "out base and byte strides must be aligned to two elements");
+  CombineParams p{};
+  p.ws_o = reinterpret_cast<const char*>(c.ws_o);
+  p.s_wo_split = c.ws_o_stride_split;
+  p.s_wo_tok = c.ws_o_stride_token;
+  p.s_wo_head = c.ws_o_stride_head;
+  p.ws_lse = reinterpret_cast<const char*>(c.ws_lse);
+  p.s_wl_split = c.ws_lse_stride_split;
+  p.s_wl_tok = c.ws_lse_stride_token;
+  p.s_wl_head = c.ws_lse_stride_head;
+  p.out = static_cast<char*>(c.out);
+  p.s_out_tok = c.out_stride_token;
+  p.s_out_head = c.out_stride_head;
+  p.out_dtype = c.out_dtype;
+  p.lse_out = lse_out;
+  p.s_lo_tok = lse_stride_token;
+  p.s_lo_head = lse_stride_head;
+  p.qsl = c.query_start_loc;
+  p.num_reqs = c.num_reqs;
+  p.num_tokens = c.num_tokens;
+  p.num_q_heads = c.num_q_heads;
+  p.num_splits = c.num_splits;
+  if (split_source != nullptr) {
+    p.seq_lens = split_source->seq_lens;
+    p.bq = split_source->bq;
+    p.window = split_source->window;
+    p.causal = split_source->causal;
+  }
+  const hipError_t err = launch_combine_kernel(p, stream);
+  if (err != hipSuccess) {
+    return fail(PTH_ATTN_ECUDA, std::string("combine launch: ") + hipGetErrorString(err));
+  }
+  return PTH_ATTN_OK;
+}
+
+}  // namespace pa
+
+// ----------------------------------------------------------------- C ABI
+namespace {
+template <class T>
+bool abi_matches(const T* a) {
+  return a->abi_version == PTH_ATTN_ABI_VERSION &&
+         a->struct_bytes == static_cast<int32_t>(sizeof(T));
+}
+
+int32_t check_args_abi(const PthAttnArgs* args) {
+  PA_REQUIRE(args != nullptr, "args is NULL");
+  PA_REQUIRE(args->abi_version == PTH_ATTN_ABI_VERSION,
+             "abi_version " + std::to_string(args->abi_version) +
+                 " != library ABI " + std::to_string(PTH_ATTN_ABI_VERSION));
+  PA_REQUIRE(args->struct_bytes == static_cast<int32_t>(sizeof(PthAttnArgs)),
+             "struct_bytes " + std::to_string(args->struct_bytes) +
+                 " != sizeof(PthAttnArgs) " + std::to_string(sizeof(PthAttnArgs)));
+  return PTH_ATTN_OK;
+}
+
+PthAttnCombineArgs combine_of(const PthAttnArgs& a) {
+  PthAttnCombineArgs c{};
+  c.abi_version = PTH_ATTN_ABI_VERSION;
+  c.struct_bytes = static_cast<int32_t>(sizeof(PthAttnCombineArgs));
+  c.ws_o = a.ws_o;
+  c.ws_o_stride_split = a.ws_o_stride_split;
+  c.ws_o_stride_token = a.ws_o_stride_token;
+  c.ws_o_stride_head = a.ws_o_stride_head;
+  c.ws_lse = a.ws_lse;
+  c.ws_lse_stride_split = a.ws_lse_stride_split;
+  c.ws_lse_stride_token = a.ws_lse_stride_token;
+  c.ws_lse_stride_head = a.ws_lse_stride_head;
+  c.out = a.out;
+  c.out_dtype = a.out_dtype;
+  c.out_stride_token = a.out_stride_token;
+  c.out_stride_head = a.out_stride_head;
+  c.query_start_loc = a.query_start_loc;
+  c.num_reqs = a.num_reqs;
+  c.num_tokens = a.num_tokens;
+  c.num_q_heads = a.num_q_heads;
+  c.head_size = a.head_size;
+  c.num_splits = a.num_splits;
+  return c;
+}
+}  // namespace
+
+extern "C" {
+
+int32_t pth_attn_abi_version(void) { return PTH_ATTN_ABI_VERSION; }
+int32_t pth_attn_attn_args_bytes(void) { return static_cast<int32_t>(sizeof(PthAttnArgs)); }
+int32_t pth_attn_combine_args_bytes(void) {
+  return static_cast<int32_t>(sizeof(PthAttnCombineArgs));
+}
+int32_t pth_attn_options_bytes(void) { return static_cast<int32_t>(sizeof(PthAttnOptions)); }
+int32_t pth_attn_has_cuda(void) { return 1; }
+const char* pth_attn_last_error(void) { return pa::last_error(); }
+
+int32_t pth_attn_tiling(int32_t head_size, int32_t bq, int32_t group,
+                        int32_t* n_tile, int32_t* sub_tile, int32_t* wn) {
+  pa::clear_error();
+  PA_REQUIRE(head_size == 128, "head_size must be 128 (the only D built)");
+  PA_REQUIRE(bq >= 1 && group >= 1, "bq and group must be >= 1");
+  PA_REQUIRE(n_tile && sub_tile && wn, "output pointers must be non-NULL");
+  PA_REQUIRE(static_cast<int64_t>(bq) * group <= 64, "bq * G exceeds 64 rows");
+  *n_tile = pa::kTileTokens;
+  *sub_tile = pa::kChunkTokens;
+  *wn = (bq * group + pa::kRowsPerWave - 1) / pa::kRowsPerWave;
+  return PTH_ATTN_OK;
+}
+
+int32_t pth_attn_attention_ex(const PthAttnArgs* args,
+                              const PthAttnOptions* options, void* stream) {
+  pa::clear_error();
+  const int32_t rc = check_args_abi(args);
+  if (rc != PTH_ATTN_OK) return rc;
+  int32_t loader = 0;
+  if (options != nullptr) {
+    PA_REQUIRE(abi_matches(options), "options: abi_version/struct_bytes mismatch");
+    loader = options->loader;
+  }
+  return pa::launch_attention(*args, loader, static_cast<hipStream_t>(stream),
+                              nullptr, 0, 0);
+}
+
+int32_t pth_attn_attention(const PthAttnArgs* args, void* stream) {
+  return pth_attn_attention_ex(args, nullptr, stream);
+}
+
+int32_t pth_attn_combine(const PthAttnCombineArgs* args, void* stream) {
+  pa::clear_error();
+  PA_REQUIRE(args != nullptr, "args is NULL");
+  PA_REQUIRE(abi_matches(args), "abi_version/struct_bytes mismatch");
+  return pa::launch_combine(*args, static_cast<hipStream_t>(stream), nullptr, 0, 0, nullptr);
+}
+
+int32_t pth_attn_attention_lse(const PthAttnArgs* args, float* lse,
+                               int64_t lse_stride_token,
+                               int64_t lse_stride_head, void* stream) {
+  pa::clear_error();
+  int32_t rc = check_args_abi(args);
+  if (rc != PTH_ATTN_OK) return rc;
+  PA_REQUIRE(lse != nullptr, "lse must be non-NULL");
+  PA_REQUIRE(args->out != nullptr, "out must be non-NULL");
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  rc = pa::launch_attention(*args, 0, st, lse, lse_stride_token, lse_stride_head);
+  if (rc != PTH_ATTN_OK || args->num_splits == 1) return rc;
+  return pa::launch_combine(combine_of(*args), st, lse, lse_stride_token, lse_stride_head,
+                            args);
+}
+
+}  // extern "C"
