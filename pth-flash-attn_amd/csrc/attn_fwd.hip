@@ -45,6 +45,10 @@
 
 #include "attn_internal.h"
 
+#ifndef PA_PAGED_INFLIGHT
+#define PA_PAGED_INFLIGHT 2
+#endif
+
 namespace pa {
 namespace {
 
@@ -113,6 +117,49 @@ struct Chunk {
 };
 
 // Lane n of every 16-lane row, broadcast to the row (DPP row_newbcast).
+// Waves per work-group of the attention kernel: one per KV head of a decode
+// tile, so the 8 cells of a token (8 x 264 contiguous bytes for NHD pages)
+// are read by one CU.
+constexpr int kFwdWaves = 8;
+// LDS staging of the paged path: two 32-key chunk slots per wave, each
+// [K: 32 x 128 B | V: 32 x 128 B | k_scale x 32, v_scale x 32].
+constexpr int kSlotK = 0;
+constexpr int kSlotV = 4096;
+constexpr int kSlotScale = 8192;
+constexpr int kSlotBytes = 8192 + 256;
+// Direct-to-LDS loads of one chunk: 4 for K, 4 for V, 1 for the scales.
+constexpr int kDmaPerChunk = 9;
+
+// s_waitcnt with only the vector-memory counter (<= n outstanding) or only
+// the LDS counter (0 outstanding). Inline asm with a memory clobber, so the
+// compiler neither moves memory operations across it nor drops it: the
+// direct-to-LDS loads are not tracked against later LDS reads by the
+// compiler's own wait insertion.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+__device__ __forceinline__ void wait_lgkmcnt0() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+// One 16-byte (or 4-byte) global -> LDS copy per lane: lane i's bytes land at
+// lds + 16 i (4 i). `lds` must be wave-uniform.
+__device__ __forceinline__ void dma16(const char* g, char* lds) {
+  __builtin_amdgcn_global_load_lds(
+      (const void __attribute__((address_space(1)))*)(g),
+      (void __attribute__((address_space(3)))*)(lds), 16, 0, 0);
+}
+__device__ __forceinline__ void dma4(const char* g, char* lds) {
+  __builtin_amdgcn_global_load_lds(
+      (const void __attribute__((address_space(1)))*)(g),
+      (void __attribute__((address_space(3)))*)(lds), 4, 0, 0);
+}
+
+// K/V rows in a slot are 128 bytes; their 16-byte pieces are stored in the
+// order piece ^ (key & 7), so the reads below (8 keys at the same piece per
+// 8 lanes for K, one key per 16 lanes for V) touch distinct banks.
+__device__ __forceinline__ int swz(int key, int piece) { return 128 * key + 16 * (piece ^ (key & 7)); }
+
 template <int N>
 __device__ __forceinline__ float row_bcast(float x) {
   return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x),
@@ -126,287 +173,335 @@ __device__ __forceinline__ const char* at(const CacheStream& s, int64_t page,
 }
 
 // One work unit: rows [16 rg, 16 rg + 16) of row tile t, KV head kvh, split
-// s of the row tile's `live` splits.
-template <bool kWindow, bool kPaged16, bool kF16Q>
-__device__ __forceinline__ void run_unit(const AttnParams& p, const RowTile& t, int s,
-                                         int live, int kvh, int rg, int lane) {
-  const int G = p.group;
-  const int rows = t.num_tok * G;
-  const int row0 = rg * kRowsPerWave;
-  if (row0 >= rows) return;
+// Read-only inputs (query_start_loc, seq_lens, block_table) are read through
+// the constant address space: a wave-uniform index then becomes a scalar
+// load, which is tracked by lgkmcnt and never makes the wave wait for its
+// vector loads in flight.
+__device__ __forceinline__ int32_t ld_ro(const int32_t* base, int64_t i) {
+  return ((const int32_t __attribute__((address_space(4)))*)(base))[i];
+}
 
-  const int r16 = lane & 15;
-  const int g = lane >> 4;
-  const int row = row0 + r16;
-  const bool vrow = row < rows;
-  const int tok = static_cast<int>(p.g_div.div(static_cast<uint32_t>(vrow ? row : row0)));
-  const int head = kvh * G + ((vrow ? row : row0) - tok * G);
-  const int64_t qtok = static_cast<int64_t>(t.q_start) + t.tok_begin + tok;
+// Cursor over the unit table of one wave: the current 64-request chunk, with
+// the inclusive prefix of units per lane. Units are requested in increasing
+// order, so the cursor only moves forward.
+struct Cursor {
+  int r0 = -64;  // first request of the chunk
+  int u0 = 0;    // units before the chunk
+  int u1 = 0;    // units through the chunk
+  int incl = 0;  // per lane: inclusive prefix within the chunk
+  bool end = false;
+};
+
+// Finds unit u (>= every unit asked before on this cursor). False when u is
+// past the table. On success req is the request and u_loc the unit's index
+// within the request.
+template <bool kWindow>
+__device__ __forceinline__ bool find_unit(const AttnParams& p, Cursor& cu, int u, int lane,
+                                          int& req, int& u_loc) {
   const int window = kWindow ? p.window : 0;
   const bool causal = kWindow ? (p.causal != 0) : true;
-  const int lo = key_lo(t, t.tok_begin + tok, window);
-  const int hi = key_hi(t, t.tok_begin + tok, window, causal);
+  while (!cu.end && u >= cu.u1) {
+    cu.r0 += 64;
+    cu.u0 = cu.u1;
+    if (cu.r0 >= p.num_reqs) {
+      cu.end = true;
+      break;
+    }
+    const int r = cu.r0 + lane;
+    int units = 0;
+    if (r < p.num_reqs) {
+      const int ql = p.qsl[r + 1] - p.qsl[r];
+      units = request_row_tiles(ql, p.bq) *
+              request_splits(ql, p.seq_lens[r], p.bq, window, causal, p.num_splits) * p.n_hu;
+    }
+    int incl = units;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int v = __shfl_up(incl, d);
+      if (lane >= d) incl += v;
+    }
+    cu.incl = incl;
+    cu.u1 = cu.u0 + __builtin_amdgcn_readlane(incl, 63);
+  }
+  if (cu.end) return false;
+  const int local = u - cu.u0;
+  const int j = static_cast<int>(__popcll(__ballot(cu.incl <= local)));
+  const int excl = j > 0 ? __builtin_amdgcn_readlane(cu.incl, j - 1) : 0;
+  req = cu.r0 + j;
+  u_loc = local - excl;
+  return true;
+}
 
-  // Key bounds of the wave's real rows (uniform): first and last token.
-  const int wrow_end = (row0 + kRowsPerWave < rows ? row0 + kRowsPerWave : rows);
-  const int tok_first = static_cast<int>(p.g_div.div(row0));
-  const int tok_last = static_cast<int>(p.g_div.div(wrow_end - 1));
-  const int w_lo_min = key_lo(t, t.tok_begin + tok_first, window);
-  const int w_lo_max = key_lo(t, t.tok_begin + tok_last, window);
-  const int w_hi_min = key_hi(t, t.tok_begin + tok_first, window, causal);
-  const int w_hi_max = key_hi(t, t.tok_begin + tok_last, window, causal);
+// Everything about one work unit that is uniform across the wave.
+struct Unit {
+  RowTile t;
+  int s, live, kvh, rg;
+  int rows;      // query rows of the row tile (num_tok * G)
+  int row0;      // first row of this wave (16 rg)
+  bool has_rows;  // row0 < rows
+  int ld_lo, ld_hi;  // keys the wave reads: [ld_lo, ld_hi)
+  int c_begin;       // first chunk (32-aligned)
+  int n_chunks;
+  int w_lo_max, w_hi_min;  // a chunk outside [w_lo_max, w_hi_min] needs the mask
+};
 
-  // Split of the row tile's KV tiles (the same for every wave of the tile).
-  const int rbeg = kWindow ? range_begin(t, window) : 0;
-  const int rend = range_end(t, window, causal);
+template <bool kWindow>
+__device__ __forceinline__ void make_unit(const AttnParams& p, int req, int u_loc, Unit& U) {
+  const int window = kWindow ? p.window : 0;
+  const bool causal = kWindow ? (p.causal != 0) : true;
+  const int q_start = ld_ro(p.qsl, req);
+  const int q_len = ld_ro(p.qsl, req + 1) - q_start;
+  const int seq_len = ld_ro(p.seq_lens, req);
+  U.live = request_splits(q_len, seq_len, p.bq, window, causal, p.num_splits);
+  const int hu = u_loc % p.n_hu;
+  const int t2 = u_loc / p.n_hu;
+  U.s = t2 % U.live;
+  U.t = request_tile(req, q_start, q_len, seq_len, p.bq, t2 / U.live);
+  U.kvh = static_cast<int>(p.rg_div.div(hu));
+  U.rg = hu - U.kvh * static_cast<int>(p.rg_div.d);
+  const int G = p.group;
+  U.rows = U.t.num_tok * G;
+  U.row0 = U.rg * kRowsPerWave;
+  U.has_rows = U.row0 < U.rows;
+  U.n_chunks = 0;
+  if (!U.has_rows) return;
+  const int wrow_end = U.row0 + kRowsPerWave < U.rows ? U.row0 + kRowsPerWave : U.rows;
+  const int tok_first = U.t.tok_begin + static_cast<int>(p.g_div.div(U.row0));
+  const int tok_last = U.t.tok_begin + static_cast<int>(p.g_div.div(wrow_end - 1));
+  const int w_lo_min = key_lo(U.t, tok_first, window);
+  U.w_lo_max = key_lo(U.t, tok_last, window);
+  U.w_hi_min = key_hi(U.t, tok_first, window, causal);
+  const int w_hi_max = key_hi(U.t, tok_last, window, causal);
+  // The row tile's KV tiles, cut into the request's live splits.
+  const int rbeg = kWindow ? range_begin(U.t, window) : 0;
+  const int rend = range_end(U.t, window, causal);
   const int ft = first_kv_tile(rbeg);
   const int nt = kv_tile_count(rbeg, rend);
-  const bool split_out = p.num_splits > 1;
-  if (split_out && s == live - 1 && vrow) {
-    // Splits [live, S) of this request hold no key of these rows: lse = -inf,
-    // so that any combine over all S splits skips them.
-    char* lse_row = reinterpret_cast<char*>(p.ws_lse) + qtok * p.s_wl_tok +
-                    static_cast<int64_t>(head) * p.s_wl_head;
-    for (int s2 = live + g; s2 < p.num_splits; s2 += 4)
-      *reinterpret_cast<float*>(lse_row + s2 * p.s_wl_split) = kNegInf;
-  }
   int tb, te;
-  split_range(s, live, nt, tb, te);
-  // Keys this wave reads: its split's tiles, clipped to its rows' keys.
-  const int c_split_lo = (ft + tb) * kTileTokens;
-  const int c_split_hi = (ft + te) * kTileTokens;
-  const int ld_lo = c_split_lo > w_lo_min ? c_split_lo : w_lo_min;
-  const int ld_hi = c_split_hi < w_hi_max + 1 ? c_split_hi : w_hi_max + 1;
-  const int c_begin = ld_lo & ~(kChunkTokens - 1);
+  split_range(U.s, U.live, nt, tb, te);
+  const int c_lo = (ft + tb) * kTileTokens, c_hi = (ft + te) * kTileTokens;
+  U.ld_lo = c_lo > w_lo_min ? c_lo : w_lo_min;
+  U.ld_hi = c_hi < w_hi_max + 1 ? c_hi : w_hi_max + 1;
+  U.c_begin = U.ld_lo & ~(kChunkTokens - 1);
+  U.n_chunks = U.c_begin < U.ld_hi ? (U.ld_hi - U.c_begin + kChunkTokens - 1) / kChunkTokens : 0;
+}
 
-  // Q^T as the B operand: qb[j] holds Q[row][32 g + 8 j .. + 8].
-  bf16x8 qb[4], qb_lo[4];
-  {
-    const char* qrow = p.q + qtok * p.s_q_tok + static_cast<int64_t>(head) * p.s_q_head;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      u32x4 raw = vrow ? *reinterpret_cast<const u32x4*>(qrow + 2 * (32 * g + 8 * j))
-                       : (u32x4){0u, 0u, 0u, 0u};
-      if constexpr (kF16Q) {
-        // fp16 q = hi + lo with hi = bf16(q), lo = bf16(q - hi): exact, because
-        // an fp16 significand has 11 bits and each bf16 holds 8.
-        const f16x8 h = __builtin_bit_cast(f16x8, raw);
-        bf16x8 a, b;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float f = static_cast<float>(h[e]);
-          const __bf16 fh = static_cast<__bf16>(f);
-          a[e] = fh;
-          b[e] = static_cast<__bf16>(f - static_cast<float>(fh));
-        }
-        qb[j] = a;
-        qb_lo[j] = b;
-      } else {
-        qb[j] = __builtin_bit_cast(bf16x8, raw);
-      }
-    }
-  }
+// Per-lane view of the unit's rows: lane l holds row row0 + (l % 16).
+struct Lanes {
+  int r16, g;
+  bool vrow;
+  int head;
+  int64_t qtok;
+  int lo, hi;
+};
 
-  const int req = t.req;
-  const int32_t* bt_row = p.block_table + static_cast<int64_t>(req) * p.bt_stride;
-  const int BS = static_cast<int>(p.bs_div.d);
+// The one scale a lane holds for a chunk (see read_chunk): the K scales of
+// lanes r < 8 are pre-multiplied by softmax_scale * log2(e) before the row
+// broadcast.
+__device__ __forceinline__ float scale_factor(int r16, float scale_log2) {
+  return r16 < 8 ? scale_log2 : 1.0f;
+}
 
-  // Lane (r, g) also loads ONE scale: k_scale of key tv(r) for r < 8, v_scale
-  // of key tv(r - 8) for r >= 8; a row broadcast hands them to the row.
-  const int sc_e = r16 & 7;
-  const CacheStream& sc_stream = r16 < 8 ? p.ks : p.vs;
+template <bool kWindow>
+__device__ __forceinline__ Lanes unit_lanes(const AttnParams& p, const Unit& U, int lane) {
+  const int window = kWindow ? p.window : 0;
+  const bool causal = kWindow ? (p.causal != 0) : true;
+  Lanes L;
+  L.r16 = lane & 15;
+  L.g = lane >> 4;
+  const int row = U.row0 + L.r16;
+  L.vrow = row < U.rows;
+  const int rr = L.vrow ? row : U.row0;
+  const int tok = static_cast<int>(p.g_div.div(static_cast<uint32_t>(rr)));
+  L.head = U.kvh * p.group + (rr - tok * p.group);
+  L.qtok = static_cast<int64_t>(U.t.q_start) + U.t.tok_begin + tok;
+  L.lo = key_lo(U.t, U.t.tok_begin + tok, window);
+  L.hi = key_hi(U.t, U.t.tok_begin + tok, window, causal);
+  return L;
+}
 
-  auto load_chunk = [&](int c, Chunk& ch) {
-    if constexpr (kPaged16) {
-      // BS % 16 == 0: the 16 keys of each half-chunk share one page (uniform).
-      int64_t page[2];
-      int slot0[2];
+// Q^T as the B operand of QK: qb[j] holds Q[row][32 g + 8 j .. + 8] in bf16
+// (and, for an fp16 q, qlo[j] the exact remainder q - bf16(q)). load_q_raw
+// issues the four 16-byte loads; q_operands converts them.
+__device__ __forceinline__ void load_q_raw(const AttnParams& p, const Lanes& L, u32x4 (&raw)[4]) {
+  const char* qrow = p.q + L.qtok * p.s_q_tok + static_cast<int64_t>(L.head) * p.s_q_head;
 #pragma unroll
-      for (int sub = 0; sub < 2; ++sub) {
-        const int c16 = c + 16 * sub;
-        page[sub] = 0;
-        slot0[sub] = 0;
-        if (c16 < ld_hi && c16 + 16 > ld_lo) {
-          const int blk = static_cast<int>(p.bs_div.div(c16));
-          slot0[sub] = c16 - blk * BS;
-          page[sub] = bt_row[blk];
-        }
-        const int tk = c16 + r16;
-        const bool ok = tk >= ld_lo && tk < ld_hi;
-        const char* kp = at(p.k, page[sub], slot0[sub] + r16, kvh) + 32 * g;
-        ch.k[sub][0] = ok ? (u32x4)(*reinterpret_cast<const u32x4_a4*>(kp)) : (u32x4){0u, 0u, 0u, 0u};
-        ch.k[sub][1] = ok ? (u32x4)(*reinterpret_cast<const u32x4_a4*>(kp + 16)) : (u32x4){0u, 0u, 0u, 0u};
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int tv = c16 + 4 * g + i;
-          const bool okv = tv >= ld_lo && tv < ld_hi;
-          const char* vp = at(p.v, page[sub], slot0[sub] + 4 * g + i, kvh) + 8 * r16;
-          ch.v[4 * sub + i] = okv ? (u32x2)(*reinterpret_cast<const u32x2_a4*>(vp)) : (u32x2){0u, 0u};
-        }
-      }
-      const int sub_e = sc_e >> 2;
-      const int ts = c + 16 * sub_e + 4 * g + (sc_e & 3);
-      const bool oks = ts >= ld_lo && ts < ld_hi;
-      const int64_t pg = sub_e ? page[1] : page[0];
-      const int sl = (sub_e ? slot0[1] : slot0[0]) + 4 * g + (sc_e & 3);
-      ch.sc = oks ? *reinterpret_cast<const float*>(at(sc_stream, pg, sl, kvh)) : 0.0f;
-    } else {
-#pragma unroll
-      for (int sub = 0; sub < 2; ++sub) {
-        const int c16 = c + 16 * sub;
-        const int tk = c16 + r16;
-        u32x4 k0 = {0u, 0u, 0u, 0u}, k1 = {0u, 0u, 0u, 0u};
-        if (tk >= ld_lo && tk < ld_hi) {
-          const int blk = static_cast<int>(p.bs_div.div(tk));
-          const char* kp = at(p.k, bt_row[blk], tk - blk * BS, kvh) + 32 * g;
-          k0 = *reinterpret_cast<const u32x4_a4*>(kp);
-          k1 = *reinterpret_cast<const u32x4_a4*>(kp + 16);
-        }
-        ch.k[sub][0] = k0;
-        ch.k[sub][1] = k1;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int tv = c16 + 4 * g + i;
-          u32x2 vv = {0u, 0u};
-          if (tv >= ld_lo && tv < ld_hi) {
-            const int blk = static_cast<int>(p.bs_div.div(tv));
-            vv = *reinterpret_cast<const u32x2_a4*>(at(p.v, bt_row[blk], tv - blk * BS, kvh) + 8 * r16);
-          }
-          ch.v[4 * sub + i] = vv;
-        }
-      }
-      const int ts = c + 16 * (sc_e >> 2) + 4 * g + (sc_e & 3);
-      float scv = 0.0f;
-      if (ts >= ld_lo && ts < ld_hi) {
-        const int blk = static_cast<int>(p.bs_div.div(ts));
-        scv = *reinterpret_cast<const float*>(at(sc_stream, bt_row[blk], ts - blk * BS, kvh));
-      }
-      ch.sc = scv;
-    }
-  };
+  for (int j = 0; j < 4; ++j)
+    raw[j] = L.vrow ? *reinterpret_cast<const u32x4*>(qrow + 2 * (32 * L.g + 8 * j))
+                    : (u32x4){0u, 0u, 0u, 0u};
+}
 
-  f32x4 o[8];
+template <bool kF16Q>
+__device__ __forceinline__ void q_operands(const u32x4 (&raw)[4], bf16x8 (&qb)[4],
+                                           bf16x8 (&qlo)[4]) {
 #pragma unroll
-  for (int j = 0; j < 8; ++j) o[j] = (f32x4){0.f, 0.f, 0.f, 0.f};
-  float m = kNegInf;
-  float l = 0.0f;
-  const float scale_log2 = p.scale_log2;
-
-  auto compute_chunk = [&](int c, const Chunk& ch) {
-    const float ks[8] = {row_bcast<0>(ch.sc), row_bcast<1>(ch.sc), row_bcast<2>(ch.sc),
-                         row_bcast<3>(ch.sc), row_bcast<4>(ch.sc), row_bcast<5>(ch.sc),
-                         row_bcast<6>(ch.sc), row_bcast<7>(ch.sc)};
-    const float vs[8] = {row_bcast<8>(ch.sc),  row_bcast<9>(ch.sc),  row_bcast<10>(ch.sc),
-                         row_bcast<11>(ch.sc), row_bcast<12>(ch.sc), row_bcast<13>(ch.sc),
-                         row_bcast<14>(ch.sc), row_bcast<15>(ch.sc)};
-    float sc[8];
-#pragma unroll
-    for (int sub = 0; sub < 2; ++sub) {
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const u32x4& w = ch.k[sub][j >> 1];
-        const bf16x8 a = (j & 1) ? i8x8_to_bf16(w[2], w[3]) : i8x8_to_bf16(w[0], w[1]);
-        acc = mfma(a, qb[j], acc);
-        if constexpr (kF16Q) acc = mfma(a, qb_lo[j], acc);
-      }
-#pragma unroll
-      for (int i = 0; i < 4; ++i) sc[4 * sub + i] = acc[i] * (ks[4 * sub + i] * scale_log2);
-    }
-    const bool need_mask = c < w_lo_max || c + kChunkTokens - 1 > w_hi_min;
-    if (need_mask) {
+  for (int j = 0; j < 4; ++j) {
+    if constexpr (kF16Q) {
+      // fp16 q = hi + lo with hi = bf16(q), lo = bf16(q - hi): exact, since an
+      // fp16 significand has 11 bits and each bf16 holds 8.
+      const f16x8 h = __builtin_bit_cast(f16x8, raw[j]);
+      bf16x8 a, b;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const int tv = c + 16 * (e >> 2) + 4 * g + (e & 3);
-        if (tv < lo || tv > hi) sc[e] = kNegInf;
+        const float f = static_cast<float>(h[e]);
+        const __bf16 fh = static_cast<__bf16>(f);
+        a[e] = fh;
+        b[e] = static_cast<__bf16>(f - static_cast<float>(fh));
       }
-    }
-    float mx = sc[0];
-#pragma unroll
-    for (int e = 1; e < 8; ++e) mx = fmaxf(mx, sc[e]);
-    mx = xor_max(mx);
-    const float m_new = fmaxf(m, mx);
-    const float m_use = m_new == kNegInf ? 0.0f : m_new;
-    const float alpha = __builtin_amdgcn_exp2f(m - m_use);
-    float pv[8];
-    float lsum = 0.0f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float pe = __builtin_amdgcn_exp2f(sc[e] - m_use);
-      lsum += pe;
-      pv[e] = pe * vs[e];
-    }
-    l = l * alpha + lsum;
-    m = m_new;
-    // P = hi + lo in bf16 (16 significant bits together): a single bf16 P
-    // would carry a 2^-9 relative error straight into the output whenever the
-    // softmax is peaked (short contexts, early causal rows).
-    bf16x8 p_hi, p_lo;
-#pragma unroll
-    for (int e = 0; e < 8; e += 2) {
-      const bf16x2 h = pack_bf16(pv[e], pv[e + 1]);
-      const uint32_t hb = __builtin_bit_cast(uint32_t, h);
-      const float h0 = __builtin_bit_cast(float, hb << 16);
-      const float h1 = __builtin_bit_cast(float, hb & 0xffff0000u);
-      const bf16x2 lw = pack_bf16(pv[e] - h0, pv[e + 1] - h1);
-      p_hi[e] = h[0];
-      p_hi[e + 1] = h[1];
-      p_lo[e] = lw[0];
-      p_lo[e + 1] = lw[1];
-    }
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      o[j] *= alpha;
-      const bf16x8 vcol = column_to_bf16(ch.v, j);
-      o[j] = mfma(vcol, p_hi, o[j]);
-      o[j] = mfma(vcol, p_lo, o[j]);
-    }
-  };
-
-  // Two-buffer pipeline: the loads of chunk c + 32 are in flight while chunk
-  // c is computed.
-  if (c_begin < ld_hi) {
-    Chunk ca, cb;
-    int c = c_begin;
-    load_chunk(c, ca);
-    while (true) {
-      if (c + kChunkTokens < ld_hi) load_chunk(c + kChunkTokens, cb);
-      compute_chunk(c, ca);
-      c += kChunkTokens;
-      if (c >= ld_hi) break;
-      if (c + kChunkTokens < ld_hi) load_chunk(c + kChunkTokens, ca);
-      compute_chunk(c, cb);
-      c += kChunkTokens;
-      if (c >= ld_hi) break;
+      qb[j] = a;
+      qlo[j] = b;
+    } else {
+      qb[j] = __builtin_bit_cast(bf16x8, raw[j]);
+      qlo[j] = qb[j];
     }
   }
+}
 
-  const float l_tot = xor_sum(l);
+template <bool kF16Q>
+__device__ __forceinline__ void load_q(const AttnParams& p, const Lanes& L, bf16x8 (&qb)[4],
+                                       bf16x8 (&qlo)[4]) {
+  u32x4 raw[4];
+  load_q_raw(p, L, raw);
+  q_operands<kF16Q>(raw, qb, qlo);
+}
+
+// Online-softmax state of one wave's 16 rows.
+struct State {
+  f32x4 o[8];  // o[j][i] = O[row][32 g + 8 i + j] (unnormalised)
+  float m;     // running max (log2 units), equal in the 4 lanes of a row
+  float l;     // this lane's part of the running sum
+};
+
+__device__ __forceinline__ void state_reset(State& st) {
+#pragma unroll
+  for (int j = 0; j < 8; ++j) st.o[j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  st.m = kNegInf;
+  st.l = 0.0f;
+}
+
+// One 32-key chunk starting at key c: S = K Q^T, mask, online softmax, O += V P.
+// The reference max m only moves when a row's chunk max exceeds it by more
+// than kRescaleSlack (log2 units): p = 2^(s - m) then stays <= 2^8, exact
+// in fp32 accumulation and bf16 hi + lo, and the 32 multiplies of the O
+// rescale are skipped for every chunk where no row's max grew that much (all
+// chunks but a few at the start of a long row). The result is the same
+// softmax: the final normalisation divides the common factor out.
+constexpr float kRescaleSlack = 8.0f;
+
+template <bool kF16Q>
+__device__ __forceinline__ void compute_chunk(const Unit& U, const Lanes& L, int c,
+                                              const Chunk& ch, const bf16x8 (&qb)[4],
+                                              const bf16x8 (&qlo)[4], float scl,
+                                              State& st) {
+  const float sc1 = ch.sc * scl;
+  const float ks[8] = {row_bcast<0>(sc1), row_bcast<1>(sc1), row_bcast<2>(sc1),
+                       row_bcast<3>(sc1), row_bcast<4>(sc1), row_bcast<5>(sc1),
+                       row_bcast<6>(sc1), row_bcast<7>(sc1)};
+  const float vs[8] = {row_bcast<8>(sc1),  row_bcast<9>(sc1),  row_bcast<10>(sc1),
+                       row_bcast<11>(sc1), row_bcast<12>(sc1), row_bcast<13>(sc1),
+                       row_bcast<14>(sc1), row_bcast<15>(sc1)};
+  float sc[8];
+#pragma unroll
+  for (int sub = 0; sub < 2; ++sub) {
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const u32x4& w = ch.k[sub][j >> 1];
+      const bf16x8 a = (j & 1) ? i8x8_to_bf16(w[2], w[3]) : i8x8_to_bf16(w[0], w[1]);
+      acc = mfma(a, qb[j], acc);
+      if constexpr (kF16Q) acc = mfma(a, qlo[j], acc);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sc[4 * sub + i] = acc[i] * ks[4 * sub + i];
+  }
+  if (c < U.w_lo_max || c + kChunkTokens - 1 > U.w_hi_min) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int key = c + 16 * (e >> 2) + 4 * L.g + (e & 3);
+      if (key < L.lo || key > L.hi) sc[e] = kNegInf;
+    }
+  }
+  float mx = sc[0];
+#pragma unroll
+  for (int e = 1; e < 8; ++e) mx = fmaxf(mx, sc[e]);
+  mx = xor_max(mx);
+  const bool grow = mx > st.m + kRescaleSlack;  // -inf + 8 = -inf: the first live chunk grows
+  if (__ballot(grow) != 0) {
+    // Rows that keep m (also an all-masked row at m = -inf) scale by 1.
+    const float alpha = grow ? __builtin_amdgcn_exp2f(st.m - mx) : 1.0f;
+    st.l *= alpha;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) st.o[j] *= alpha;
+    st.m = grow ? mx : st.m;
+  }
+  const float m_use = st.m == kNegInf ? 0.0f : st.m;
+  float pv[8];
+  float lsum = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float pe = __builtin_amdgcn_exp2f(sc[e] - m_use);
+    lsum += pe;
+    pv[e] = pe > 0.0f ? pe * vs[e] : 0.0f;  // a masked key's scale may be any bits
+  }
+  st.l += lsum;
+  // P = hi + lo in bf16 (16 significant bits together): a single bf16 P would
+  // carry a 2^-9 relative error into the output whenever the softmax is
+  // peaked (short contexts, early causal rows).
+  bf16x8 p_hi, p_lo;
+#pragma unroll
+  for (int e = 0; e < 8; e += 2) {
+    const bf16x2 h = pack_bf16(pv[e], pv[e + 1]);
+    const uint32_t hb = __builtin_bit_cast(uint32_t, h);
+    const float h0 = __builtin_bit_cast(float, hb << 16);
+    const float h1 = __builtin_bit_cast(float, hb & 0xffff0000u);
+    const bf16x2 lw = pack_bf16(pv[e] - h0, pv[e + 1] - h1);
+    p_hi[e] = h[0];
+    p_hi[e + 1] = h[1];
+    p_lo[e] = lw[0];
+    p_lo[e + 1] = lw[1];
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const bf16x8 vcol = column_to_bf16(ch.v, j);
+    st.o[j] = mfma(vcol, p_hi, st.o[j]);
+    st.o[j] = mfma(vcol, p_lo, st.o[j]);
+  }
+}
+
+// Writes the unit's result: out (S == 1) or the split partials (S > 1), and
+// -inf into the request's unused split slots [live, S) when this is its last
+// live split.
+__device__ __forceinline__ void epilogue(const AttnParams& p, const Unit& U, const Lanes& L,
+                                         const State& st) {
+  const float l_tot = xor_sum(st.l);
+  if (!L.vrow) return;
+  const int g = L.g;
   const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
-  if (!vrow) return;
   float res[32];  // res[8 i + j] = column 32 g + 8 i + j
 #pragma unroll
   for (int j = 0; j < 8; ++j)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) res[8 * i + j] = o[j][i] * inv;
-  const float lse2 = l_tot > 0.0f ? m + __builtin_amdgcn_logf(l_tot) : kNegInf;
+    for (int i = 0; i < 4; ++i) res[8 * i + j] = st.o[j][i] * inv;
+  const float lse2 = l_tot > 0.0f ? st.m + __builtin_amdgcn_logf(l_tot) : kNegInf;
+  const int64_t head = L.head;
 
-  if (split_out) {
-    char* dst = reinterpret_cast<char*>(p.ws_o) + s * p.s_wo_split + qtok * p.s_wo_tok +
-                static_cast<int64_t>(head) * p.s_wo_head + 4 * 32 * g;
+  if (p.num_splits > 1) {
+    char* dst = reinterpret_cast<char*>(p.ws_o) + U.s * p.s_wo_split + L.qtok * p.s_wo_tok +
+                head * p.s_wo_head + 4 * 32 * g;
 #pragma unroll
     for (int k = 0; k < 8; ++k)
       *reinterpret_cast<f32x4*>(dst + 16 * k) =
           (f32x4){res[4 * k], res[4 * k + 1], res[4 * k + 2], res[4 * k + 3]};
-    if (g == 0) {
-      float* lse = reinterpret_cast<float*>(reinterpret_cast<char*>(p.ws_lse) + s * p.s_wl_split +
-                                            qtok * p.s_wl_tok +
-                                            static_cast<int64_t>(head) * p.s_wl_head);
-      *lse = lse2;
+    char* lse_row = reinterpret_cast<char*>(p.ws_lse) + L.qtok * p.s_wl_tok + head * p.s_wl_head;
+    if (g == 0) *reinterpret_cast<float*>(lse_row + U.s * p.s_wl_split) = lse2;
+    if (U.s == U.live - 1) {
+      // Splits [live, S) of the request hold no key of these rows.
+      for (int s2 = U.live + g; s2 < p.num_splits; s2 += 4)
+        *reinterpret_cast<float*>(lse_row + s2 * p.s_wl_split) = kNegInf;
     }
     return;
   }
-  char* dst = p.out + qtok * p.s_out_tok + static_cast<int64_t>(head) * p.s_out_head;
+  char* dst = p.out + L.qtok * p.s_out_tok + head * p.s_out_head;
   if (p.out_dtype == PTH_ATTN_BF16) {
     dst += 2 * 32 * g;
 #pragma unroll
@@ -438,79 +533,367 @@ __device__ __forceinline__ void run_unit(const AttnParams& p, const RowTile& t, 
   }
   if (p.lse_out != nullptr && g == 0) {
     float* lo_ptr = reinterpret_cast<float*>(reinterpret_cast<char*>(p.lse_out) +
-                                             qtok * p.s_lo_tok +
-                                             static_cast<int64_t>(head) * p.s_lo_head);
+                                             L.qtok * p.s_lo_tok + head * p.s_lo_head);
     *lo_ptr = lse2 * 0.69314718055994530942f;
   }
 }
 
+// ---------------------------------------------------------------------------
+// Paged kernel (block size a multiple of 16): the 16-key halves of a chunk
+// each lie in one page. A producer walks this wave's chunk sequence -- all
+// chunks of its units, in order -- and keeps the next two in flight in the
+// wave's two LDS slots with direct-to-LDS loads; the consumer computes the
+// chunk before them from registers. The producer crosses unit boundaries, so
+// a new unit's first chunks are already in flight while the previous unit
+// finishes: the pipeline does not drain between units.
+struct Producer {
+  Cursor cur;
+  int next_u;
+  Unit U;
+  int k;  // next chunk of U to issue
+  bool done;
+  // Per-lane byte offsets, within a 16-key group of one page, of the bytes
+  // this lane copies (K and V: two key rows, one per 8-key half; one scale).
+  uint32_t off_k[2], off_v[2], off_s;
+};
 
-// The persistent worker loop (see the header comment for the unit table).
-template <bool kWindow, bool kPaged16, bool kF16Q>
-__global__ __launch_bounds__(256, 2) void attn_fwd_d128(const AttnParams p) {
+// The per-lane offsets of unit U's KV head (they only depend on the head).
+__device__ __forceinline__ void producer_offsets(const AttnParams& p, Producer& P, int lane) {
+  const int kq = lane >> 3, piece = lane & 7;
+  const int64_t sw = 16 * (piece ^ kq);  // row r's piece c goes to LDS position c ^ (r & 7)
+  const int64_t kvh = P.U.kvh;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int64_t key = 8 * h + kq;
+    P.off_k[h] = static_cast<uint32_t>(key * p.k.s_slot + kvh * p.k.s_head + sw);
+    P.off_v[h] = static_cast<uint32_t>(key * p.v.s_slot + kvh * p.v.s_head + sw);
+  }
+  const CacheStream& st = lane < 32 ? p.ks : p.vs;
+  P.off_s = static_cast<uint32_t>((lane & 15) * st.s_slot + kvh * st.s_head);
+}
+
+// Moves the producer to its next chunk; false when the wave has no more.
+template <bool kWindow>
+__device__ __forceinline__ bool producer_next(const AttnParams& p, Producer& P, int lane,
+                                              int num_workers) {
+  while (!P.done && P.k >= P.U.n_chunks) {
+    int req, u_loc;
+    if (!find_unit<kWindow>(p, P.cur, P.next_u, lane, req, u_loc)) {
+      P.done = true;
+      break;
+    }
+    P.next_u += num_workers;
+    make_unit<kWindow>(p, req, u_loc, P.U);
+    P.k = 0;
+    if (P.U.n_chunks > 0) producer_offsets(p, P, lane);
+  }
+  return !P.done;
+}
+
+// Issues the 9 direct-to-LDS loads of the producer's next chunk into `slot`:
+// 4 x 1 KB of K, 4 x 1 KB of V (8 keys x 128 bytes each) and the 64 scales.
+// Addresses are a uniform base (page and slot arithmetic on the scalar unit)
+// plus the lane's 32-bit offset. Every address is inside the cache: a key
+// outside the unit's range reads another slot of the same page (or page 0)
+// and is masked by the consumer, so every chunk issues exactly kDmaPerChunk
+// loads.
+__device__ __forceinline__ void issue_chunk(const AttnParams& p, Producer& P, char* slot, int lane) {
+  const Unit& U = P.U;
+  const int c = U.c_begin + kChunkTokens * P.k;
+  ++P.k;
+  const int BS = static_cast<int>(p.bs_div.d);
+  const int64_t bt0 = static_cast<int64_t>(U.t.req) * p.bt_stride;
+  const char* kb[2];
+  const char* vb[2];
+  const char* ksb[2];
+  const char* vsb[2];
+#pragma unroll
+  for (int sub = 0; sub < 2; ++sub) {
+    const int c16 = c + 16 * sub;
+    int64_t page = 0;
+    int64_t slot0 = 0;
+    if (c16 < U.ld_hi && c16 + 16 > U.ld_lo) {
+      const int blk = static_cast<int>(p.bs_div.div(c16));
+      slot0 = c16 - blk * BS;
+      page = ld_ro(p.block_table, bt0 + blk);
+    }
+    kb[sub] = p.k.base + page * p.k.s_block + slot0 * p.k.s_slot;
+    vb[sub] = p.v.base + page * p.v.s_block + slot0 * p.v.s_slot;
+    ksb[sub] = p.ks.base + page * p.ks.s_block + slot0 * p.ks.s_slot;
+    vsb[sub] = p.vs.base + page * p.vs.s_block + slot0 * p.vs.s_slot;
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    dma16(kb[i >> 1] + P.off_k[i & 1], slot + kSlotK + 1024 * i);
+    dma16(vb[i >> 1] + P.off_v[i & 1], slot + kSlotV + 1024 * i);
+  }
+  const int sub = (lane >> 4) & 1;
+  const char* sb = lane < 32 ? (sub ? ksb[1] : ksb[0]) : (sub ? vsb[1] : vsb[0]);
+  dma4(sb + P.off_s, slot + kSlotScale);
+}
+
+// LDS reads of a slot are inline asm: the compiler then neither orders them
+// after every direct-to-LDS load in flight (its alias analysis cannot tell
+// the slots apart, so it would wait for all of them) nor moves them; the
+// waits are explicit (wait_vmcnt before, chunk_ready after).
+__device__ __forceinline__ uint32_t lds_offset(const char* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
+      (const __attribute__((address_space(3))) char*)(p)));
+}
+template <int kOff>
+__device__ __forceinline__ u32x4 ds_read16(uint32_t a) {
+  u32x4 v;
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(a), "n"(kOff));
+  return v;
+}
+template <int kOff>
+__device__ __forceinline__ u32x2 ds_read8(uint32_t a) {
+  u32x2 v;
+  asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(v) : "v"(a), "n"(kOff));
+  return v;
+}
+__device__ __forceinline__ float ds_read4(uint32_t a) {
+  float v;
+  asm volatile("ds_read_b32 %0, %1" : "=v"(v) : "v"(a));
+  return v;
+}
+// Waits for the slot reads and ties every register they wrote to the wait,
+// so that no use is scheduled before it.
+__device__ __forceinline__ void chunk_ready(Chunk& ch) {
+  asm volatile("s_waitcnt lgkmcnt(0)"
+               : "+v"(ch.k[0][0]), "+v"(ch.k[0][1]), "+v"(ch.k[1][0]), "+v"(ch.k[1][1]),
+                 "+v"(ch.v[0]), "+v"(ch.v[1]), "+v"(ch.v[2]), "+v"(ch.v[3]), "+v"(ch.v[4]),
+                 "+v"(ch.v[5]), "+v"(ch.v[6]), "+v"(ch.v[7]), "+v"(ch.sc)
+               :
+               : "memory");
+}
+
+// Per-lane LDS offsets of the consumer's reads within a slot (lane (r, g):
+// K of keys r and 16 + r at pieces 2g, 2g + 1; V of the 8 keys tv(e) at
+// bytes 8r; one scale), independent of the chunk.
+struct ReadOffsets {
+  uint32_t k[2];  // + 2048 for keys 16..31
+  uint32_t v[4];  // index e & 3; + 2048 for e >= 4
+  uint32_t s;
+};
+
+__device__ __forceinline__ ReadOffsets read_offsets(int lane) {
+  const int r16 = lane & 15, g = lane >> 4;
+  ReadOffsets o;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) o.k[h] = kSlotK + swz(r16, 2 * g + h);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) o.v[q] = kSlotV + swz(4 * g + q, r16 >> 1) + 8 * (r16 & 1);
+  const int e = r16 & 7;
+  const int key = 16 * (e >> 2) + 4 * g + (e & 3);
+  o.s = kSlotScale + (r16 < 8 ? 0 : 128) + 4 * key;
+  return o;
+}
+
+__device__ __forceinline__ void read_chunk(uint32_t base, const ReadOffsets& o, Chunk& ch) {
+  const uint32_t k0 = base + o.k[0], k1 = base + o.k[1];
+  ch.k[0][0] = ds_read16<0>(k0);
+  ch.k[0][1] = ds_read16<0>(k1);
+  ch.k[1][0] = ds_read16<2048>(k0);
+  ch.k[1][1] = ds_read16<2048>(k1);
+  const uint32_t v0 = base + o.v[0], v1 = base + o.v[1], v2 = base + o.v[2], v3 = base + o.v[3];
+  ch.v[0] = ds_read8<0>(v0);
+  ch.v[1] = ds_read8<0>(v1);
+  ch.v[2] = ds_read8<0>(v2);
+  ch.v[3] = ds_read8<0>(v3);
+  ch.v[4] = ds_read8<2048>(v0);
+  ch.v[5] = ds_read8<2048>(v1);
+  ch.v[6] = ds_read8<2048>(v2);
+  ch.v[7] = ds_read8<2048>(v3);
+  ch.sc = ds_read4(base + o.s);
+  chunk_ready(ch);
+}
+
+template <int kInFlight>
+__device__ __forceinline__ void wait_chunk(int inflight) {
+  // Chunks issued after the one about to be read: inflight - 1, each
+  // kDmaPerChunk loads (any other vector memory operation issued after it
+  // only makes the wait stricter).
+  if constexpr (kInFlight >= 2) {
+    if (inflight >= 2) {
+      wait_vmcnt<kDmaPerChunk>();
+      return;
+    }
+  }
+  wait_vmcnt<0>();
+}
+
+template <bool kWindow, bool kF16Q, int kInFlight>
+__global__ __launch_bounds__(kFwdWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void attn_fwd_paged(const AttnParams p) {
+  __shared__ __attribute__((aligned(16))) char lds_all[kFwdWaves * kInFlight * kSlotBytes];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int worker = blockIdx.x * kWaves + wave;
-  const int num_workers = gridDim.x * kWaves;
-  const int R = p.num_reqs;
-  const int n_hu = p.n_hu;
-  const int bq = p.bq;
-  const int window = kWindow ? p.window : 0;
-  const bool causal = kWindow ? (p.causal != 0) : true;
+  char* lds = lds_all + wave * kInFlight * kSlotBytes;
+  const uint32_t lds_base = lds_offset(lds);
+  const ReadOffsets ro = read_offsets(lane);
+  const float scl = scale_factor(lane & 15, p.scale_log2);
+  const int worker = blockIdx.x * kFwdWaves + wave;
+  const int num_workers = gridDim.x * kFwdWaves;
 
-  // The current 64-request chunk of the unit table: lane j describes request
-  // chunk_r0 + j; incl is the inclusive prefix of units within the chunk.
-  int chunk_r0 = -64;
-  int chunk_u0 = 0, chunk_u1 = 0;
-  int incl = 0;
-  for (int u = worker;; u += num_workers) {
-    bool done = false;
-    while (u >= chunk_u1) {
-      chunk_r0 += 64;
-      chunk_u0 = chunk_u1;
-      if (chunk_r0 >= R) {
-        done = true;
+  Producer P;
+  P.next_u = worker;
+  P.U.n_chunks = 0;
+  P.k = 0;
+  P.done = false;
+  int inflight = 0;  // chunks issued and not yet consumed
+  int slot_w = 0;    // slot the producer fills next
+#pragma unroll
+  for (int i = 0; i < kInFlight; ++i) {
+    if (producer_next<kWindow>(p, P, lane, num_workers)) {
+      issue_chunk(p, P, lds + slot_w * kSlotBytes, lane);
+      ++inflight;
+      slot_w = slot_w + 1 == kInFlight ? 0 : slot_w + 1;
+    }
+  }
+
+  Cursor cur;
+  int next_u = worker;
+  Unit U;
+  Lanes L;
+  State st;
+  bf16x8 qb[4], qlo[4];
+  int ck = 0;
+  bool have = false;
+  int slot_r = 0;
+  while (true) {
+    if (!have || ck >= U.n_chunks) {
+      if (have) epilogue(p, U, L, st);
+      have = false;
+      int req, u_loc;
+      while (find_unit<kWindow>(p, cur, next_u, lane, req, u_loc)) {
+        next_u += num_workers;
+        make_unit<kWindow>(p, req, u_loc, U);
+        if (!U.has_rows) continue;
+        L = unit_lanes<kWindow>(p, U, lane);
+        state_reset(st);
+        if (U.n_chunks == 0) {  // no key of these rows in this split
+          epilogue(p, U, L, st);
+          continue;
+        }
+        have = true;
         break;
       }
-      const int r = chunk_r0 + lane;
-      int units = 0;
-      if (r < R) {
-        const int ql = p.qsl[r + 1] - p.qsl[r];
-        units = request_row_tiles(ql, bq) *
-                request_splits(ql, p.seq_lens[r], bq, window, causal, p.num_splits) * n_hu;
-      }
-      incl = units;
-#pragma unroll
-      for (int d = 1; d < 64; d <<= 1) {
-        const int v = __shfl_up(incl, d);
-        if (lane >= d) incl += v;
-      }
-      chunk_u1 = chunk_u0 + __builtin_amdgcn_readlane(incl, 63);
+      if (!have) break;
+      load_q<kF16Q>(p, L, qb, qlo);
+      // A compiler-visible wait for Q here (vmcnt(0): it also drains this
+      // unit's chunks in flight, once per unit) keeps the compiler from
+      // re-waiting for Q, with vmcnt(0), before every chunk of the loop.
+      __builtin_amdgcn_s_waitcnt(0x0F70);
+      ck = 0;
     }
-    if (done) break;
-    const int local = u - chunk_u0;
-    const int j = static_cast<int>(__popcll(__ballot(incl <= local)));
-    const int excl = j > 0 ? __builtin_amdgcn_readlane(incl, j - 1) : 0;
-    const int u_loc = local - excl;
-    const int req = chunk_r0 + j;
-    const int q_start = p.qsl[req];
-    const int q_len = p.qsl[req + 1] - q_start;
-    const int seq_len = p.seq_lens[req];
-    const int live = request_splits(q_len, seq_len, bq, window, causal, p.num_splits);
-    const int hu = u_loc % n_hu;
-    const int t2 = u_loc / n_hu;
-    const int s = t2 % live;
-    const int rt = t2 / live;
-    const RowTile t = request_tile(req, q_start, q_len, seq_len, bq, rt);
-    const int kvh = static_cast<int>(p.rg_div.div(hu));
-    const int rg = hu - kvh * static_cast<int>(p.rg_div.d);
-    run_unit<kWindow, kPaged16, kF16Q>(p, t, s, live, kvh, rg, lane);
+    wait_chunk<kInFlight>(inflight);
+    Chunk ch;
+    read_chunk(lds_base + slot_r * kSlotBytes, ro, ch);  // returns once the reads landed
+    --inflight;
+    slot_r = slot_r + 1 == kInFlight ? 0 : slot_r + 1;
+    if (producer_next<kWindow>(p, P, lane, num_workers)) {
+      issue_chunk(p, P, lds + slot_w * kSlotBytes, lane);
+      ++inflight;
+      slot_w = slot_w + 1 == kInFlight ? 0 : slot_w + 1;
+    }
+    compute_chunk<kF16Q>(U, L, U.c_begin + kChunkTokens * ck, ch, qb, qlo, scl, st);
+    ++ck;
   }
 }
 
-template <bool W, bool P, bool F>
-hipError_t launch_one(const AttnParams& p, dim3 grid, hipStream_t stream) {
-  hipLaunchKernelGGL((attn_fwd_d128<W, P, F>), grid, dim3(kWaves * 64), 0, stream, p);
+// ---------------------------------------------------------------------------
+// Generic kernel (any block size): one page lookup per key, loads straight to
+// registers, the next chunk in flight while the current one is computed.
+template <bool kWindow>
+__device__ __forceinline__ void load_chunk_generic(const AttnParams& p, const Unit& U,
+                                                   const Lanes& L, int c, Chunk& ch) {
+  const int BS = static_cast<int>(p.bs_div.d);
+  const int32_t* bt = p.block_table + static_cast<int64_t>(U.t.req) * p.bt_stride;
+  const int r16 = L.r16, g = L.g;
+#pragma unroll
+  for (int sub = 0; sub < 2; ++sub) {
+    const int tk = c + 16 * sub + r16;
+    u32x4 k0 = {0u, 0u, 0u, 0u}, k1 = {0u, 0u, 0u, 0u};
+    if (tk >= U.ld_lo && tk < U.ld_hi) {
+      const int blk = static_cast<int>(p.bs_div.div(tk));
+      const char* kp = at(p.k, bt[blk], tk - blk * BS, U.kvh) + 32 * g;
+      k0 = *reinterpret_cast<const u32x4_a4*>(kp);
+      k1 = *reinterpret_cast<const u32x4_a4*>(kp + 16);
+    }
+    ch.k[sub][0] = k0;
+    ch.k[sub][1] = k1;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int tv = c + 16 * sub + 4 * g + i;
+      u32x2 vv = {0u, 0u};
+      if (tv >= U.ld_lo && tv < U.ld_hi) {
+        const int blk = static_cast<int>(p.bs_div.div(tv));
+        vv = *reinterpret_cast<const u32x2_a4*>(at(p.v, bt[blk], tv - blk * BS, U.kvh) + 8 * r16);
+      }
+      ch.v[4 * sub + i] = vv;
+    }
+  }
+  const int e = r16 & 7;
+  const int ts = c + 16 * (e >> 2) + 4 * g + (e & 3);
+  float scv = 0.0f;
+  if (ts >= U.ld_lo && ts < U.ld_hi) {
+    const int blk = static_cast<int>(p.bs_div.div(ts));
+    scv = *reinterpret_cast<const float*>(at(r16 < 8 ? p.ks : p.vs, bt[blk], ts - blk * BS, U.kvh));
+  }
+  ch.sc = scv;
+}
+
+template <bool kWindow, bool kF16Q>
+__global__ __launch_bounds__(kFwdWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void attn_fwd_generic(const AttnParams p) {
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int worker = blockIdx.x * kFwdWaves + wave;
+  const int num_workers = gridDim.x * kFwdWaves;
+  const float scl = scale_factor(lane & 15, p.scale_log2);
+  Cursor cur;
+  for (int u = worker;; u += num_workers) {
+    int req, u_loc;
+    if (!find_unit<kWindow>(p, cur, u, lane, req, u_loc)) break;
+    Unit U;
+    make_unit<kWindow>(p, req, u_loc, U);
+    if (!U.has_rows) continue;
+    const Lanes L = unit_lanes<kWindow>(p, U, lane);
+    State st;
+    state_reset(st);
+    if (U.n_chunks > 0) {
+      bf16x8 qb[4], qlo[4];
+      load_q<kF16Q>(p, L, qb, qlo);
+      Chunk ca, cb;
+      int k = 0;
+      load_chunk_generic<kWindow>(p, U, L, U.c_begin, ca);
+      while (true) {
+        const int c = U.c_begin + kChunkTokens * k;
+        if (k + 1 < U.n_chunks) load_chunk_generic<kWindow>(p, U, L, c + kChunkTokens, cb);
+        compute_chunk<kF16Q>(U, L, c, ca, qb, qlo, scl, st);
+        if (++k >= U.n_chunks) break;
+        if (k + 1 < U.n_chunks) load_chunk_generic<kWindow>(p, U, L, c + 2 * kChunkTokens, ca);
+        compute_chunk<kF16Q>(U, L, c + kChunkTokens, cb, qb, qlo, scl, st);
+        if (++k >= U.n_chunks) break;
+      }
+    }
+    epilogue(p, U, L, st);
+  }
+}
+
+// Chunks in flight per wave on the paged path (LDS slots per wave).
+constexpr int kPagedInFlight = PA_PAGED_INFLIGHT;
+
+template <bool W, bool F>
+hipError_t launch_paged(const AttnParams& p, dim3 grid, hipStream_t stream) {
+  hipLaunchKernelGGL((attn_fwd_paged<W, F, kPagedInFlight>), grid, dim3(kFwdWaves * 64), 0,
+                     stream, p);
+  return hipGetLastError();
+}
+template <bool W, bool F>
+hipError_t launch_generic(const AttnParams& p, dim3 grid, hipStream_t stream) {
+  hipLaunchKernelGGL((attn_fwd_generic<W, F>), grid, dim3(kFwdWaves * 64), 0, stream, p);
   return hipGetLastError();
 }
 
@@ -518,16 +901,16 @@ hipError_t launch_one(const AttnParams& p, dim3 grid, hipStream_t stream) {
 
 hipError_t launch_fwd_kernel(const AttnParams& p, dim3 grid, bool windowed,
                              bool paged16, bool q_f16, hipStream_t stream) {
-  if (windowed) {
-    if (paged16) return q_f16 ? launch_one<true, true, true>(p, grid, stream)
-                              : launch_one<true, true, false>(p, grid, stream);
-    return q_f16 ? launch_one<true, false, true>(p, grid, stream)
-                 : launch_one<true, false, false>(p, grid, stream);
+  if (paged16) {
+    if (windowed) return q_f16 ? launch_paged<true, true>(p, grid, stream)
+                               : launch_paged<true, false>(p, grid, stream);
+    return q_f16 ? launch_paged<false, true>(p, grid, stream)
+                 : launch_paged<false, false>(p, grid, stream);
   }
-  if (paged16) return q_f16 ? launch_one<false, true, true>(p, grid, stream)
-                            : launch_one<false, true, false>(p, grid, stream);
-  return q_f16 ? launch_one<false, false, true>(p, grid, stream)
-               : launch_one<false, false, false>(p, grid, stream);
+  if (windowed) return q_f16 ? launch_generic<true, true>(p, grid, stream)
+                             : launch_generic<true, false>(p, grid, stream);
+  return q_f16 ? launch_generic<false, true>(p, grid, stream)
+               : launch_generic<false, false>(p, grid, stream);
 }
 
 }  // namespace pa

@@ -89,7 +89,9 @@ int32_t launch_combine(const PthAttnCombineArgs& c, hipStream_t stream,
                        int64_t lse_stride_head, const PthAttnArgs* split_source);
 
 // Per-variant kernel launches (attn_fwd.hip, attn_combine.hip).
-// Work-groups of kWaves waves that fill the device once (CUs x 2).
+// Waves per work-group of the attention kernel, and the work-groups that
+// fill the device once (one per CU).
+constexpr int32_t kFwdWavesPerGroup = 8;
 int32_t resident_workgroups();
 hipError_t launch_fwd_kernel(const AttnParams& p, dim3 grid, bool windowed,
                              bool paged16, bool q_f16, hipStream_t stream);

@@ -44,7 +44,7 @@ CacheStream cache_stream(const PthAttnStream& s) {
 }  // namespace
 
 int32_t resident_workgroups() {
-  // 8 waves per CU (2 per SIMD at <= 256 VGPRs) = 2 work-groups of kWaves.
+  // 8 waves per CU (2 per SIMD at <= 256 VGPRs) = one 8-wave work-group.
   constexpr int kMaxDevices = 64;
   static int32_t cached[kMaxDevices] = {};
   int dev = 0;
@@ -54,7 +54,7 @@ int32_t resident_workgroups() {
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
       cus <= 0)
     return 0;
-  const int32_t wgs = cus * 2;
+  const int32_t wgs = cus;
   if (dev < kMaxDevices) cached[dev] = wgs;
   return wgs;
 }
@@ -187,7 +187,7 @@ int32_t launch_attention(const PthAttnArgs& a, int32_t loader,
       a.num_q_tiles > 0 ? a.num_q_tiles
                         : static_cast<int64_t>(a.num_tokens) / a.bq + a.num_reqs;
   const int64_t unit_bound = tile_bound * a.num_splits * p.n_hu;
-  const int64_t wg_need = (unit_bound + kWaves - 1) / kWaves;
+  const int64_t wg_need = (unit_bound + kFwdWavesPerGroup - 1) / kFwdWavesPerGroup;
   const int32_t wg_fill = resident_workgroups();
   PA_REQUIRE(wg_fill > 0, "cannot query the compute-unit count of the current device");
   PA_REQUIRE(unit_bound < 0x7fffffff, "the work table exceeds 2^31 - 1 units");
