@@ -1,6 +1,6 @@
 // attn_geometry.h -- integer geometry of one attention launch, shared by the
 // gfx950 kernels and the host launcher (and compiled by g++ for the CPU
-// tests through geometry_capi.cpp).
+// tests by tests/cpp/test_geometry.cpp).
 //
 // It answers, with integer arithmetic only:
 //   * division by run-time divisors (block size, GQA group, row-tile height)
