@@ -100,13 +100,39 @@ __device__ __forceinline__ f32x4 mfma(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
+// Reductions over the 4 lanes of a query row (lanes r, r + 16, r + 32,
+// r + 48) with the gfx950 cross-row swaps. With both operands holding x,
+// permlane16_swap returns {x of rows 0, 0, 2, 2 ; x of rows 1, 1, 3, 3} and
+// permlane32_swap {x of the low half twice ; x of the high half twice}, so
+// combining the pair gives the xor-16 (xor-32) partner's value; both lanes
+// of a pair combine the same two values in the same order, so all 4 lanes
+// end with the same result. The two results are copied to named scalars
+// before use: indexing the returned pair inside a bit cast reads element 0
+// twice with this compiler.
+struct SwapPair {
+  float a, b;
+};
+__device__ __forceinline__ SwapPair swap_rows16(float x) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, x);
+  auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  const uint32_t r0 = r[0], r1 = r[1];
+  return {__builtin_bit_cast(float, r0), __builtin_bit_cast(float, r1)};
+}
+__device__ __forceinline__ SwapPair swap_halves(float x) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, x);
+  auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  const uint32_t r0 = r[0], r1 = r[1];
+  return {__builtin_bit_cast(float, r0), __builtin_bit_cast(float, r1)};
+}
 __device__ __forceinline__ float xor_max(float x) {
-  x = fmaxf(x, __shfl_xor(x, 16));
-  return fmaxf(x, __shfl_xor(x, 32));
+  const SwapPair a = swap_rows16(x);
+  const SwapPair b = swap_halves(fmaxf(a.a, a.b));
+  return fmaxf(b.a, b.b);
 }
 __device__ __forceinline__ float xor_sum(float x) {
-  x += __shfl_xor(x, 16);
-  return x + __shfl_xor(x, 32);
+  const SwapPair a = swap_rows16(x);
+  const SwapPair b = swap_halves(a.a + a.b);
+  return b.a + b.b;
 }
 
 // The cache bytes of one 32-key chunk for one lane.
@@ -385,7 +411,8 @@ __device__ __forceinline__ void state_reset(State& st) {
 // in fp32 accumulation and bf16 hi + lo, and the 32 multiplies of the O
 // rescale are skipped for every chunk where no row's max grew that much (all
 // chunks but a few at the start of a long row). The result is the same
-// softmax: the final normalisation divides the common factor out.
+// softmax: the final normalisation divides the common factor out. A row's
+// first chunk with a visible key always sets m.
 constexpr float kRescaleSlack = 8.0f;
 
 template <bool kF16Q>
@@ -397,10 +424,12 @@ __device__ __forceinline__ void compute_chunk(const Unit& U, const Lanes& L, int
   const float ks[8] = {row_bcast<0>(sc1), row_bcast<1>(sc1), row_bcast<2>(sc1),
                        row_bcast<3>(sc1), row_bcast<4>(sc1), row_bcast<5>(sc1),
                        row_bcast<6>(sc1), row_bcast<7>(sc1)};
-  const float vs[8] = {row_bcast<8>(sc1),  row_bcast<9>(sc1),  row_bcast<10>(sc1),
-                       row_bcast<11>(sc1), row_bcast<12>(sc1), row_bcast<13>(sc1),
-                       row_bcast<14>(sc1), row_bcast<15>(sc1)};
-  float sc[8];
+  float vs[8] = {row_bcast<8>(sc1),  row_bcast<9>(sc1),  row_bcast<10>(sc1),
+                 row_bcast<11>(sc1), row_bcast<12>(sc1), row_bcast<13>(sc1),
+                 row_bcast<14>(sc1), row_bcast<15>(sc1)};
+  const bool fresh = st.m == kNegInf;
+  const float m_use = fresh ? 0.0f : st.m;
+  float t[8];  // score - m_use (log2 units)
 #pragma unroll
   for (int sub = 0; sub < 2; ++sub) {
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -412,36 +441,43 @@ __device__ __forceinline__ void compute_chunk(const Unit& U, const Lanes& L, int
       if constexpr (kF16Q) acc = mfma(a, qlo[j], acc);
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) sc[4 * sub + i] = acc[i] * ks[4 * sub + i];
+    for (int i = 0; i < 4; ++i) t[4 * sub + i] = fmaf(acc[i], ks[4 * sub + i], -m_use);
   }
   if (c < U.w_lo_max || c + kChunkTokens - 1 > U.w_hi_min) {
+    // A key outside the row's range (or the request) gets p = 0 and a zero
+    // V scale: its cache bytes may be any bits, a scale included.
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const int key = c + 16 * (e >> 2) + 4 * L.g + (e & 3);
-      if (key < L.lo || key > L.hi) sc[e] = kNegInf;
+      if (key < L.lo || key > L.hi) {
+        t[e] = kNegInf;
+        vs[e] = 0.0f;
+      }
     }
   }
-  float mx = sc[0];
+  float mx = t[0];
 #pragma unroll
-  for (int e = 1; e < 8; ++e) mx = fmaxf(mx, sc[e]);
+  for (int e = 1; e < 8; ++e) mx = fmaxf(mx, t[e]);
   mx = xor_max(mx);
-  const bool grow = mx > st.m + kRescaleSlack;  // -inf + 8 = -inf: the first live chunk grows
+  const bool grow = fresh ? mx > kNegInf : mx > kRescaleSlack;
   if (__ballot(grow) != 0) {
-    // Rows that keep m (also an all-masked row at m = -inf) scale by 1.
-    const float alpha = grow ? __builtin_amdgcn_exp2f(st.m - mx) : 1.0f;
+    // Rows that keep m (also rows with no visible key yet) scale by 1.
+    const float alpha = grow && !fresh ? __builtin_amdgcn_exp2f(-mx) : 1.0f;
     st.l *= alpha;
 #pragma unroll
     for (int j = 0; j < 8; ++j) st.o[j] *= alpha;
-    st.m = grow ? mx : st.m;
+    const float shift = grow ? mx : 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) t[e] -= shift;
+    st.m = grow ? m_use + mx : st.m;
   }
-  const float m_use = st.m == kNegInf ? 0.0f : st.m;
   float pv[8];
   float lsum = 0.0f;
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    const float pe = __builtin_amdgcn_exp2f(sc[e] - m_use);
+    const float pe = __builtin_amdgcn_exp2f(t[e]);
     lsum += pe;
-    pv[e] = pe > 0.0f ? pe * vs[e] : 0.0f;  // a masked key's scale may be any bits
+    pv[e] = pe * vs[e];
   }
   st.l += lsum;
   // P = hi + lo in bf16 (16 significant bits together): a single bf16 P would
@@ -468,40 +504,61 @@ __device__ __forceinline__ void compute_chunk(const Unit& U, const Lanes& L, int
   }
 }
 
-// Writes the unit's result: out (S == 1) or the split partials (S > 1), and
-// -inf into the request's unused split slots [live, S) when this is its last
-// live split.
-__device__ __forceinline__ void epilogue(const AttnParams& p, const Unit& U, const Lanes& L,
-                                         const State& st) {
+// A finished unit's result, held in registers until it is stored.
+struct Finished {
+  float res[32];  // res[8 i + j] = normalised O[row][32 g + 8 i + j]
+  float lse2;     // log2-sum-exp of the row, -inf without a visible key
+  int64_t qtok;
+  int head, g;
+  bool vrow;
+  int s;
+};
+
+__device__ __forceinline__ void finish(const Unit& U, const Lanes& L, const State& st,
+                                       Finished& f) {
   const float l_tot = xor_sum(st.l);
-  if (!L.vrow) return;
-  const int g = L.g;
   const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
-  float res[32];  // res[8 i + j] = column 32 g + 8 i + j
 #pragma unroll
   for (int j = 0; j < 8; ++j)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) res[8 * i + j] = st.o[j][i] * inv;
-  const float lse2 = l_tot > 0.0f ? st.m + __builtin_amdgcn_logf(l_tot) : kNegInf;
-  const int64_t head = L.head;
+    for (int i = 0; i < 4; ++i) f.res[8 * i + j] = st.o[j][i] * inv;
+  f.lse2 = l_tot > 0.0f ? st.m + __builtin_amdgcn_logf(l_tot) : kNegInf;
+  f.qtok = L.qtok;
+  f.head = L.head;
+  f.g = L.g;
+  f.vrow = L.vrow;
+  f.s = U.s;
+}
 
+// Stores a finished unit: out (S == 1) or the split partials (S > 1). The
+// split slots [live, S) that a request does not use are left untouched here
+// (fill_unused_splits writes them when a caller needs them).
+// Vector memory instructions store_finished issues per unit, the same for
+// every unit of a launch (the lanes without a row are masked off, never the
+// whole wave: row 0 of a unit always exists), so that the waits of the chunk
+// pipeline can count past them.
+__device__ __forceinline__ int stores_per_unit(const AttnParams& p) {
+  if (p.num_splits > 1) return 9;
+  return (p.out_dtype == PTH_ATTN_F32 ? 8 : 4) + (p.lse_out != nullptr ? 1 : 0);
+}
+
+__device__ __forceinline__ void store_finished(const AttnParams& p, const Finished& f) {
+  if (!f.vrow) return;
+  const int g = f.g;
+  const int64_t head = f.head;
   if (p.num_splits > 1) {
-    char* dst = reinterpret_cast<char*>(p.ws_o) + U.s * p.s_wo_split + L.qtok * p.s_wo_tok +
+    char* dst = reinterpret_cast<char*>(p.ws_o) + f.s * p.s_wo_split + f.qtok * p.s_wo_tok +
                 head * p.s_wo_head + 4 * 32 * g;
 #pragma unroll
     for (int k = 0; k < 8; ++k)
       *reinterpret_cast<f32x4*>(dst + 16 * k) =
-          (f32x4){res[4 * k], res[4 * k + 1], res[4 * k + 2], res[4 * k + 3]};
-    char* lse_row = reinterpret_cast<char*>(p.ws_lse) + L.qtok * p.s_wl_tok + head * p.s_wl_head;
-    if (g == 0) *reinterpret_cast<float*>(lse_row + U.s * p.s_wl_split) = lse2;
-    if (U.s == U.live - 1) {
-      // Splits [live, S) of the request hold no key of these rows.
-      for (int s2 = U.live + g; s2 < p.num_splits; s2 += 4)
-        *reinterpret_cast<float*>(lse_row + s2 * p.s_wl_split) = kNegInf;
-    }
+          (f32x4){f.res[4 * k], f.res[4 * k + 1], f.res[4 * k + 2], f.res[4 * k + 3]};
+    // The 4 lanes of a row hold the same lse2 and store it to the same place.
+    char* lse_row = reinterpret_cast<char*>(p.ws_lse) + f.qtok * p.s_wl_tok + head * p.s_wl_head;
+    *reinterpret_cast<float*>(lse_row + f.s * p.s_wl_split) = f.lse2;
     return;
   }
-  char* dst = p.out + L.qtok * p.s_out_tok + head * p.s_out_head;
+  char* dst = p.out + f.qtok * p.s_out_tok + head * p.s_out_head;
   if (p.out_dtype == PTH_ATTN_BF16) {
     dst += 2 * 32 * g;
 #pragma unroll
@@ -509,7 +566,7 @@ __device__ __forceinline__ void epilogue(const AttnParams& p, const Unit& U, con
       bf16x8 v;
 #pragma unroll
       for (int e = 0; e < 8; e += 2) {
-        const bf16x2 pr = pack_bf16(res[8 * k + e], res[8 * k + e + 1]);
+        const bf16x2 pr = pack_bf16(f.res[8 * k + e], f.res[8 * k + e + 1]);
         v[e] = pr[0];
         v[e + 1] = pr[1];
       }
@@ -521,7 +578,7 @@ __device__ __forceinline__ void epilogue(const AttnParams& p, const Unit& U, con
     for (int k = 0; k < 4; ++k) {
       f16x8 v;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) v[e] = static_cast<_Float16>(res[8 * k + e]);
+      for (int e = 0; e < 8; ++e) v[e] = static_cast<_Float16>(f.res[8 * k + e]);
       *reinterpret_cast<f16x8*>(dst + 16 * k) = v;
     }
   } else {
@@ -529,13 +586,20 @@ __device__ __forceinline__ void epilogue(const AttnParams& p, const Unit& U, con
 #pragma unroll
     for (int k = 0; k < 8; ++k)
       *reinterpret_cast<f32x4*>(dst + 16 * k) =
-          (f32x4){res[4 * k], res[4 * k + 1], res[4 * k + 2], res[4 * k + 3]};
+          (f32x4){f.res[4 * k], f.res[4 * k + 1], f.res[4 * k + 2], f.res[4 * k + 3]};
   }
-  if (p.lse_out != nullptr && g == 0) {
+  if (p.lse_out != nullptr) {
     float* lo_ptr = reinterpret_cast<float*>(reinterpret_cast<char*>(p.lse_out) +
-                                             L.qtok * p.s_lo_tok + head * p.s_lo_head);
-    *lo_ptr = lse2 * 0.69314718055994530942f;
+                                             f.qtok * p.s_lo_tok + head * p.s_lo_head);
+    *lo_ptr = f.lse2 * 0.69314718055994530942f;
   }
+}
+
+__device__ __forceinline__ void epilogue(const AttnParams& p, const Unit& U, const Lanes& L,
+                                         const State& st) {
+  Finished f;
+  finish(U, L, st, f);
+  store_finished(p, f);
 }
 
 // ---------------------------------------------------------------------------
@@ -552,24 +616,47 @@ struct Producer {
   Unit U;
   int k;  // next chunk of U to issue
   bool done;
-  // Per-lane byte offsets, within a 16-key group of one page, of the bytes
-  // this lane copies (K and V: two key rows, one per 8-key half; one scale).
+  // Cache pages and first slots of the two 16-key groups of chunk k, loaded
+  // one chunk ahead so that the issue never waits for the block table.
+  int32_t page[2];
+  int32_t slot0[2];
+  // Per-lane byte offsets within a 16-key group of one page (the cell view of
+  // the cache): K and V of two key rows (one per 8-key half), and one scale.
   uint32_t off_k[2], off_v[2], off_s;
 };
 
-// The per-lane offsets of unit U's KV head (they only depend on the head).
+// The per-lane offsets of unit U's KV head.
 __device__ __forceinline__ void producer_offsets(const AttnParams& p, Producer& P, int lane) {
-  const int kq = lane >> 3, piece = lane & 7;
-  const int64_t sw = 16 * (piece ^ kq);  // row r's piece c goes to LDS position c ^ (r & 7)
-  const int64_t kvh = P.U.kvh;
+  const uint32_t kq = lane >> 3, piece = lane & 7;
+  const uint32_t head = static_cast<uint32_t>(P.U.kvh) * p.cell_head;
+  const uint32_t sw = 16u * (piece ^ kq);  // row r's piece c goes to LDS position c ^ (r & 7)
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
-    const int64_t key = 8 * h + kq;
-    P.off_k[h] = static_cast<uint32_t>(key * p.k.s_slot + kvh * p.k.s_head + sw);
-    P.off_v[h] = static_cast<uint32_t>(key * p.v.s_slot + kvh * p.v.s_head + sw);
+    const uint32_t row = (8u * h + kq) * p.cell_slot + head + sw;
+    P.off_k[h] = row + p.cell_off[0];
+    P.off_v[h] = row + p.cell_off[1];
   }
-  const CacheStream& st = lane < 32 ? p.ks : p.vs;
-  P.off_s = static_cast<uint32_t>((lane & 15) * st.s_slot + kvh * st.s_head);
+  P.off_s = static_cast<uint32_t>(lane & 15) * p.cell_slot + head +
+            (lane < 32 ? p.cell_off[2] : p.cell_off[3]);
+}
+
+// Block-table lookup for chunk k of the producer's unit (scalar loads; a
+// 16-key group outside the unit's keys reads page 0 and is masked later).
+__device__ __forceinline__ void producer_pages(const AttnParams& p, Producer& P) {
+  const Unit& U = P.U;
+  const int c = U.c_begin + kChunkTokens * P.k;
+  const int64_t bt0 = static_cast<int64_t>(U.t.req) * p.bt_stride;
+#pragma unroll
+  for (int sub = 0; sub < 2; ++sub) {
+    const int c16 = c + 16 * sub;
+    P.page[sub] = 0;
+    P.slot0[sub] = 0;
+    if (c16 < U.ld_hi && c16 + 16 > U.ld_lo) {
+      const int blk = static_cast<int>(p.bs_div.div(c16));
+      P.slot0[sub] = c16 - blk * static_cast<int>(p.bs_div.d);
+      P.page[sub] = ld_ro(p.block_table, bt0 + blk);
+    }
+  }
 }
 
 // Moves the producer to its next chunk; false when the wave has no more.
@@ -585,51 +672,37 @@ __device__ __forceinline__ bool producer_next(const AttnParams& p, Producer& P, 
     P.next_u += num_workers;
     make_unit<kWindow>(p, req, u_loc, P.U);
     P.k = 0;
-    if (P.U.n_chunks > 0) producer_offsets(p, P, lane);
+    if (P.U.n_chunks > 0) {
+      producer_offsets(p, P, lane);
+      producer_pages(p, P);
+    }
   }
   return !P.done;
 }
 
-// Issues the 9 direct-to-LDS loads of the producer's next chunk into `slot`:
-// 4 x 1 KB of K, 4 x 1 KB of V (8 keys x 128 bytes each) and the 64 scales.
-// Addresses are a uniform base (page and slot arithmetic on the scalar unit)
-// plus the lane's 32-bit offset. Every address is inside the cache: a key
-// outside the unit's range reads another slot of the same page (or page 0)
-// and is masked by the consumer, so every chunk issues exactly kDmaPerChunk
-// loads.
+// Issues the 9 direct-to-LDS loads of the producer's chunk k into `slot`:
+// 4 x 1 KB of K, 4 x 1 KB of V (8 keys x 128 bytes each) and the 64 scales,
+// then looks up the pages of chunk k + 1. Each 16-key group's address is a
+// uniform 64-bit base (page * page stride + first slot * slot stride, on the
+// scalar unit) plus the lane's 32-bit offset. Every address is inside the
+// cache: a key outside the unit's range reads another slot of the same page
+// (or of page 0) and is masked by the consumer, so every chunk issues
+// exactly kDmaPerChunk loads.
 __device__ __forceinline__ void issue_chunk(const AttnParams& p, Producer& P, char* slot, int lane) {
-  const Unit& U = P.U;
-  const int c = U.c_begin + kChunkTokens * P.k;
-  ++P.k;
-  const int BS = static_cast<int>(p.bs_div.d);
-  const int64_t bt0 = static_cast<int64_t>(U.t.req) * p.bt_stride;
-  const char* kb[2];
-  const char* vb[2];
-  const char* ksb[2];
-  const char* vsb[2];
+  const char* base[2];
 #pragma unroll
-  for (int sub = 0; sub < 2; ++sub) {
-    const int c16 = c + 16 * sub;
-    int64_t page = 0;
-    int64_t slot0 = 0;
-    if (c16 < U.ld_hi && c16 + 16 > U.ld_lo) {
-      const int blk = static_cast<int>(p.bs_div.div(c16));
-      slot0 = c16 - blk * BS;
-      page = ld_ro(p.block_table, bt0 + blk);
-    }
-    kb[sub] = p.k.base + page * p.k.s_block + slot0 * p.k.s_slot;
-    vb[sub] = p.v.base + page * p.v.s_block + slot0 * p.v.s_slot;
-    ksb[sub] = p.ks.base + page * p.ks.s_block + slot0 * p.ks.s_slot;
-    vsb[sub] = p.vs.base + page * p.vs.s_block + slot0 * p.vs.s_slot;
-  }
+  for (int sub = 0; sub < 2; ++sub)
+    base[sub] = p.cell_base +
+                static_cast<uint64_t>(static_cast<uint32_t>(P.page[sub])) * p.cell_block +
+                static_cast<uint32_t>(P.slot0[sub]) * p.cell_slot;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    dma16(kb[i >> 1] + P.off_k[i & 1], slot + kSlotK + 1024 * i);
-    dma16(vb[i >> 1] + P.off_v[i & 1], slot + kSlotV + 1024 * i);
+    dma16(base[i >> 1] + P.off_k[i & 1], slot + kSlotK + 1024 * i);
+    dma16(base[i >> 1] + P.off_v[i & 1], slot + kSlotV + 1024 * i);
   }
-  const int sub = (lane >> 4) & 1;
-  const char* sb = lane < 32 ? (sub ? ksb[1] : ksb[0]) : (sub ? vsb[1] : vsb[0]);
-  dma4(sb + P.off_s, slot + kSlotScale);
+  dma4(((lane >> 4) & 1 ? base[1] : base[0]) + P.off_s, slot + kSlotScale);
+  ++P.k;
+  if (P.k < P.U.n_chunks) producer_pages(p, P);
 }
 
 // LDS reads of a slot are inline asm: the compiler then neither orders them
@@ -709,18 +782,22 @@ __device__ __forceinline__ void read_chunk(uint32_t base, const ReadOffsets& o, 
   chunk_ready(ch);
 }
 
-template <int kInFlight>
-__device__ __forceinline__ void wait_chunk(int inflight) {
-  // Chunks issued after the one about to be read: inflight - 1, each
-  // kDmaPerChunk loads (any other vector memory operation issued after it
-  // only makes the wait stricter).
-  if constexpr (kInFlight >= 2) {
-    if (inflight >= 2) {
-      wait_vmcnt<kDmaPerChunk>();
-      return;
-    }
+// Waits until at most `younger` vector memory operations are outstanding:
+// with in-order completion, that is until everything issued before the last
+// `younger` operations has completed. `younger` is wave-uniform; counts
+// outside the listed ones fall back to a full wait.
+__device__ __forceinline__ void wait_vmcnt_dyn(int younger) {
+  switch (younger) {
+    case 4: wait_vmcnt<4>(); break;
+    case 5: wait_vmcnt<5>(); break;
+    case 8: wait_vmcnt<8>(); break;
+    case 9: wait_vmcnt<9>(); break;
+    case 13: wait_vmcnt<13>(); break;
+    case 14: wait_vmcnt<14>(); break;
+    case 17: wait_vmcnt<17>(); break;
+    case 18: wait_vmcnt<18>(); break;
+    default: wait_vmcnt<0>(); break;
   }
-  wait_vmcnt<0>();
 }
 
 template <bool kWindow, bool kF16Q, int kInFlight>
@@ -761,9 +838,18 @@ void attn_fwd_paged(const AttnParams p) {
   int ck = 0;
   bool have = false;
   int slot_r = 0;
+  // The stores of a finished unit are issued after the wait that drains the
+  // pipeline at the unit switch: vector memory operations complete in issue
+  // order, so a store issued in front of chunks still in flight would make
+  // every wait for those chunks wait for the store as well. The waits of
+  // the chunks that were in flight before the stores count past them.
+  const int n_store = stores_per_unit(p);
+  int older_than_stores = 0;  // chunks in flight issued before the last stores
   while (true) {
     if (!have || ck >= U.n_chunks) {
-      if (have) epilogue(p, U, L, st);
+      Finished done;
+      const bool had = have;
+      if (have) finish(U, L, st, done);
       have = false;
       int req, u_loc;
       while (find_unit<kWindow>(p, cur, next_u, lane, req, u_loc)) {
@@ -771,23 +857,34 @@ void attn_fwd_paged(const AttnParams p) {
         make_unit<kWindow>(p, req, u_loc, U);
         if (!U.has_rows) continue;
         L = unit_lanes<kWindow>(p, U, lane);
-        state_reset(st);
         if (U.n_chunks == 0) {  // no key of these rows in this split
-          epilogue(p, U, L, st);
+          State empty;
+          state_reset(empty);
+          epilogue(p, U, L, empty);
           continue;
         }
         have = true;
         break;
       }
-      if (!have) break;
-      load_q<kF16Q>(p, L, qb, qlo);
+      if (have) load_q<kF16Q>(p, L, qb, qlo);
       // A compiler-visible wait for Q here (vmcnt(0): it also drains this
       // unit's chunks in flight, once per unit) keeps the compiler from
       // re-waiting for Q, with vmcnt(0), before every chunk of the loop.
       __builtin_amdgcn_s_waitcnt(0x0F70);
+      if (had) {
+        store_finished(p, done);
+        older_than_stores = inflight;
+      }
+      if (!have) break;
+      state_reset(st);
       ck = 0;
     }
-    wait_chunk<kInFlight>(inflight);
+    // Operations issued after the chunk about to be read: the next chunk's
+    // loads when it is in flight, and the last unit's stores when they were
+    // issued after this chunk's loads.
+    wait_vmcnt_dyn((kInFlight >= 2 && inflight >= 2 ? kDmaPerChunk : 0) +
+                   (older_than_stores > 0 ? n_store : 0));
+    if (older_than_stores > 0) --older_than_stores;
     Chunk ch;
     read_chunk(lds_base + slot_r * kSlotBytes, ro, ch);  // returns once the reads landed
     --inflight;
@@ -897,7 +994,48 @@ hipError_t launch_generic(const AttnParams& p, dim3 grid, hipStream_t stream) {
   return hipGetLastError();
 }
 
+// -inf into the log2-LSE slot of every split s >= live of every query row
+// (live = the splits the row's request uses), so that a combine over all S
+// splits ignores them, as the reference's launch contract requires of the
+// split partials (reference attn_args.h:38-44). One thread per (split,
+// token, head) slot of splits 1..S-1, head fastest: consecutive threads
+// write consecutive floats. Rows of padding tokens are not written.
+__global__ __launch_bounds__(256) void fill_unused_splits(const AttnParams p, int32_t num_tokens,
+                                                          int32_t num_q_heads) {
+  const int64_t per_split = static_cast<int64_t>(num_tokens) * num_q_heads;
+  const int64_t total = per_split * (p.num_splits - 1);
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int s2 = 1 + static_cast<int>(i / per_split);
+    const int64_t r = i - (s2 - 1) * per_split;
+    const int tok = static_cast<int>(r / num_q_heads);
+    const int head = static_cast<int>(r - static_cast<int64_t>(tok) * num_q_heads);
+    if (tok >= p.qsl[p.num_reqs]) continue;
+    int lo = 0, hi = p.num_reqs - 1;  // request: largest r with qsl[r] <= tok
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (p.qsl[mid] <= tok) lo = mid; else hi = mid - 1;
+    }
+    const int q_start = p.qsl[lo];
+    const int live = request_splits(p.qsl[lo + 1] - q_start, p.seq_lens[lo], p.bq, p.window,
+                                    p.causal != 0, p.num_splits);
+    if (s2 >= live)
+      *reinterpret_cast<float*>(reinterpret_cast<char*>(p.ws_lse) + s2 * p.s_wl_split +
+                                tok * p.s_wl_tok + head * p.s_wl_head) = kNegInf;
+  }
+}
+
 }  // namespace
+
+hipError_t launch_fill_unused_splits(const AttnParams& p, int32_t num_tokens,
+                                     int32_t num_q_heads, hipStream_t stream) {
+  const int64_t total = static_cast<int64_t>(num_tokens) * num_q_heads * (p.num_splits - 1);
+  if (total <= 0) return hipSuccess;
+  const int64_t blocks = (total + 255) / 256;
+  hipLaunchKernelGGL(fill_unused_splits, dim3(static_cast<unsigned>(blocks < 4096 ? blocks : 4096)),
+                     dim3(256), 0, stream, p, num_tokens, num_q_heads);
+  return hipGetLastError();
+}
 
 hipError_t launch_fwd_kernel(const AttnParams& p, dim3 grid, bool windowed,
                              bool paged16, bool q_f16, hipStream_t stream) {

@@ -35,6 +35,14 @@ struct AttnParams {
   float* lse_out;  // optional natural-log LSE of every row (S == 1 only)
   int64_t s_lo_tok, s_lo_head;
   CacheStream k, v, ks, vs;
+  // The same four streams as one array of cells, for the paged kernel: one
+  // base, common byte strides, and each stream's byte offset within a cell
+  // (K, V, k_scale, v_scale). Set when the streams share their strides (the
+  // vLLM cache: four views of one buffer); `cell` is false otherwise.
+  bool cell;
+  const char* cell_base;
+  uint32_t cell_block, cell_slot, cell_head;
+  uint32_t cell_off[4];
   const int32_t* block_table;
   int64_t bt_stride;  // elements
   const int32_t* seq_lens;
@@ -81,9 +89,13 @@ struct CombineParams {
 // Host launchers. They check their arguments, enqueue on `stream`, allocate
 // nothing and never synchronise. Return PTH_ATTN_OK, EINVAL or ECUDA; the
 // message of a failure is last_error() on the calling thread.
+// fill_unused_splits: also write -inf into the split slots [live, S) that
+// no request uses (needed when the caller combines all S splits itself; the
+// combine launched with split_source reads only the live ones).
 int32_t launch_attention(const PthAttnArgs& a, int32_t loader,
                          hipStream_t stream, float* lse_out,
-                         int64_t lse_stride_token, int64_t lse_stride_head);
+                         int64_t lse_stride_token, int64_t lse_stride_head,
+                         bool fill_unused_splits);
 int32_t launch_combine(const PthAttnCombineArgs& c, hipStream_t stream,
                        float* lse_out, int64_t lse_stride_token,
                        int64_t lse_stride_head, const PthAttnArgs* split_source);
@@ -96,6 +108,8 @@ int32_t resident_workgroups();
 hipError_t launch_fwd_kernel(const AttnParams& p, dim3 grid, bool windowed,
                              bool paged16, bool q_f16, hipStream_t stream);
 hipError_t launch_combine_kernel(const CombineParams& c, hipStream_t stream);
+hipError_t launch_fill_unused_splits(const AttnParams& p, int32_t num_tokens,
+                                     int32_t num_q_heads, hipStream_t stream);
 
 const char* last_error();
 int32_t fail(int32_t code, const std::string& msg);

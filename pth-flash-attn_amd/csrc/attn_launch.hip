@@ -8,6 +8,7 @@
 // both launch through launch_attention / launch_combine, so the op runs
 // exactly the code the C-ABI tests exercise.
 
+#include <algorithm>
 #include <cmath>
 #include <string>
 
@@ -41,6 +42,40 @@ CacheStream cache_stream(const PthAttnStream& s) {
                      s.stride_slot, s.stride_head};
 }
 
+// Fills the cell view of the four streams when they share their strides and
+// every per-lane offset the paged kernel forms (key < 16 of a 16-key group,
+// any KV head, any stream, plus a 128-byte row) fits in 32 bits.
+void set_cell_geometry(const PthAttnArgs& a, AttnParams& p) {
+  p.cell = false;
+  const PthAttnStream* st[4] = {&a.k_cache, &a.v_cache, &a.k_scale, &a.v_scale};
+  const int64_t sb = st[0]->stride_block, ss = st[0]->stride_slot, sh = st[0]->stride_head;
+  if (sb < 0 || ss < 0 || sh < 0) return;
+  uintptr_t lo = reinterpret_cast<uintptr_t>(st[0]->data);
+  for (int i = 0; i < 4; ++i) {
+    if (st[i]->stride_block != sb || st[i]->stride_slot != ss || st[i]->stride_head != sh)
+      return;
+    lo = std::min(lo, reinterpret_cast<uintptr_t>(st[i]->data));
+  }
+  const uint64_t lim = uint64_t{1} << 32;
+  uint64_t max_off = 0;
+  for (int i = 0; i < 4; ++i) {
+    const uint64_t off = reinterpret_cast<uintptr_t>(st[i]->data) - lo;
+    if (off >= lim) return;
+    p.cell_off[i] = static_cast<uint32_t>(off);
+    max_off = std::max(max_off, off);
+  }
+  const uint64_t reach = 15u * static_cast<uint64_t>(ss) +
+                         static_cast<uint64_t>(a.num_kv_heads - 1) * static_cast<uint64_t>(sh) +
+                         max_off + 128u;
+  const uint64_t slot_reach = static_cast<uint64_t>(a.block_size) * static_cast<uint64_t>(ss);
+  if (static_cast<uint64_t>(sb) >= lim || reach >= lim || slot_reach >= lim) return;
+  p.cell = true;
+  p.cell_base = reinterpret_cast<const char*>(lo);
+  p.cell_block = static_cast<uint32_t>(sb);
+  p.cell_slot = static_cast<uint32_t>(ss);
+  p.cell_head = static_cast<uint32_t>(sh);
+}
+
 }  // namespace
 
 int32_t resident_workgroups() {
@@ -68,7 +103,8 @@ void clear_error() { g_last_error.clear(); }
 
 int32_t launch_attention(const PthAttnArgs& a, int32_t loader,
                          hipStream_t stream, float* lse_out,
-                         int64_t lse_stride_token, int64_t lse_stride_head) {
+                         int64_t lse_stride_token, int64_t lse_stride_head,
+                         bool fill_unused_splits) {
   clear_error();
   PA_REQUIRE(loader >= 0 && loader <= 2,
              "options.loader must be 0 (default), 1 (separate) or 2 (cell)");
@@ -162,6 +198,7 @@ int32_t launch_attention(const PthAttnArgs& a, int32_t loader,
   p.v = cache_stream(a.v_cache);
   p.ks = cache_stream(a.k_scale);
   p.vs = cache_stream(a.v_scale);
+  set_cell_geometry(a, p);
   p.block_table = a.block_table;
   p.bt_stride = a.block_table_row_stride;
   p.seq_lens = a.seq_lens;
@@ -193,13 +230,18 @@ int32_t launch_attention(const PthAttnArgs& a, int32_t loader,
   PA_REQUIRE(unit_bound < 0x7fffffff, "the work table exceeds 2^31 - 1 units");
   const dim3 grid(static_cast<unsigned>(wg_need < wg_fill ? wg_need : wg_fill));
   const bool windowed = a.window > 0 || a.causal == 0;
-  const bool paged16 = a.block_size % 16 == 0;
+  const bool paged16 = a.block_size % 16 == 0 && p.cell;
   const hipError_t err = launch_fwd_kernel(p, grid, windowed, paged16,
                                            a.q_dtype == PTH_ATTN_F16, stream);
   if (err != hipSuccess) {
     return fail(PTH_ATTN_ECUDA, std::string("attention launch (D=128, rows=") +
                                     std::to_string(rows) + "): " +
                                     hipGetErrorString(err));
+  }
+  if (fill_unused_splits && a.num_splits > 1) {
+    const hipError_t e2 = launch_fill_unused_splits(p, a.num_tokens, a.num_q_heads, stream);
+    if (e2 != hipSuccess)
+      return fail(PTH_ATTN_ECUDA, std::string("unused-split fill launch: ") + hipGetErrorString(e2));
   }
   return PTH_ATTN_OK;
 }
@@ -346,8 +388,10 @@ int32_t pth_attn_attention_ex(const PthAttnArgs* args,
     PA_REQUIRE(abi_matches(options), "options: abi_version/struct_bytes mismatch");
     loader = options->loader;
   }
+  // A caller of this entry may combine all S splits itself
+  // (pth_attn_combine), so the unused split slots get -inf.
   return pa::launch_attention(*args, loader, static_cast<hipStream_t>(stream),
-                              nullptr, 0, 0);
+                              nullptr, 0, 0, /*fill_unused_splits=*/true);
 }
 
 int32_t pth_attn_attention(const PthAttnArgs* args, void* stream) {
@@ -370,7 +414,8 @@ int32_t pth_attn_attention_lse(const PthAttnArgs* args, float* lse,
   PA_REQUIRE(lse != nullptr, "lse must be non-NULL");
   PA_REQUIRE(args->out != nullptr, "out must be non-NULL");
   const hipStream_t st = static_cast<hipStream_t>(stream);
-  rc = pa::launch_attention(*args, 0, st, lse, lse_stride_token, lse_stride_head);
+  rc = pa::launch_attention(*args, 0, st, lse, lse_stride_token, lse_stride_head,
+                            /*fill_unused_splits=*/false);
   if (rc != PTH_ATTN_OK || args->num_splits == 1) return rc;
   return pa::launch_combine(combine_of(*args), st, lse, lse_stride_token, lse_stride_head,
                             args);

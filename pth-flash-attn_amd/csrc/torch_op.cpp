@@ -356,7 +356,8 @@ void launch_library(const Tensor& out, const Tensor& q, const Tensor& k_cache,
   const c10::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
   const hipStream_t stream =
       c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(q.get_device()).stream();
-  int32_t rc = pa::launch_attention(a, 0, stream, nullptr, 0, 0);
+  // The combine below reads only the splits each request used.
+  int32_t rc = pa::launch_attention(a, 0, stream, nullptr, 0, 0, /*fill_unused_splits=*/false);
   PFA_CHECK(rc == PTH_ATTN_OK, "attention launch: ", pa::last_error());
   if (num_splits == 1) return;
   PthAttnCombineArgs c{};

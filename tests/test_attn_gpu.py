@@ -189,6 +189,22 @@ def test_deterministic():
     assert torch.equal(l1, l2)
 
 
+@pytest.mark.parametrize("S", [7, 64, 256])
+def test_public_entry_points_combine_all_splits(S):
+    """pth_attn_attention then pth_attn_combine over ALL S splits (the
+    reference's launch contract): requests that use fewer splits than S must
+    leave -inf in their unused log2-LSE slots, which the workspace starts
+    without (it is filled with NaN)."""
+    c = Case("public-all-S", q_lens=[1, 4, 1, 2], seq_lens=[100, 3000, 17, 700], Hq=8, Hkv=2,
+             seed=21)
+    b = materialize(c, DEV)
+    out, _ = run_capi(b, num_splits=S, with_lse=False)
+    ref_out, ref_lse, valid = oracle_of(b)
+    res = compare(out, None, ref_out, ref_lse, valid)
+    print(f"  S={S} -> {res}", flush=True)
+    assert_parity(res, name=f"public S={S}", strict=False)
+
+
 # ---------------------------------------------------------------- configs 2-5
 def test_config2_batched_decode():
     """Config 2: 64 seqs, q=1, 32q/8kv, L ~ U[1k, 32k], BS 16."""
