@@ -195,6 +195,13 @@ int32_t pth_attn_attention_lse(const PthAttnArgs* args, float* lse,
                                int64_t lse_stride_token,
                                int64_t lse_stride_head, void* stream);
 
+/* Benchmark entry: the attention kernel of `args` exactly as the torch op
+ * launches it before its combine (rows whose keys form a single split are
+ * written to args->out, the others to the split partials; the unused split
+ * slots are not filled). With the combine of pth_attn_attention_lse this is
+ * the op's layer call. No counterpart in the reference's ABI. */
+int32_t pth_attn_attention_kernel(const PthAttnArgs* args, void* stream);
+
 #ifdef __cplusplus
 } /* extern "C" */
 #endif

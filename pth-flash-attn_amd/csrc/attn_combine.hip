@@ -11,14 +11,19 @@
 // or uninitialised memory) never enters an arithmetic operation; the sums run
 // in the fixed order s = 0..S-1, so the result is deterministic.
 //
-// One wave64 per (token, head) row; lane l owns columns 2 l and 2 l + 1, so a
-// split's row is one coalesced 512-byte read. Lane s loads lse_s (64 splits
-// per instruction); the weights are broadcast with readlane and the o loads
-// of 8 splits are issued before their fused multiply-adds. When the launcher
-// passes the request lengths, only the splits the attention kernel used for
-// the row's request are read (the others hold -inf by construction).
+// Few rows with many splits (shared_rows): a work-group of 4 waves takes one
+// (token, head) row: wave 0 alone, or, for a row with more than 64 splits,
+// all 4 (wave w merges the 64-split blocks w, w + 4, ... and wave 0 merges
+// the 4 results in a fixed order). Otherwise one wave per row.
+// Lane l owns columns 2 l and 2 l + 1, so a split's row is one coalesced
+// 512-byte read. Lane s loads lse_s (64 splits per instruction);
+// the weights are broadcast with readlane and the o loads of 16 splits are
+// issued before their fused multiply-adds. When the launcher
+// passes the request lengths, only the splits the attention kernel wrote for
+// the row are read (attn_stream.h), and a row with a single split is left as
+// the attention kernel wrote it to out.
 
-#include "attn_internal.h"
+#include "attn_stream.h"
 
 namespace pa {
 namespace {
@@ -28,7 +33,7 @@ typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 
 constexpr float kNegInf = -__builtin_inff();
-constexpr int kBatch = 8;
+constexpr int kBatch = 16;
 
 __device__ __forceinline__ float wave_max(float x) {
 #pragma unroll
@@ -43,15 +48,9 @@ __device__ __forceinline__ float wave_sum(float x) {
   return x;
 }
 
-__global__ __launch_bounds__(256) void combine_d128(const CombineParams c) {
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * kWaves + wave;
-  const int64_t tok = row / c.num_q_heads;
-  const int head = static_cast<int>(row - tok * c.num_q_heads);
-  if (tok >= c.num_tokens) return;
-
-  // Request of the token: the number of requests that end at or before it.
+// Request of token tok: the number of requests that end at or before it
+// (num_reqs for a padding row beyond qsl[R]).
+__device__ __forceinline__ int request_of_token(const CombineParams& c, int64_t tok, int lane) {
   int r = 0;
   for (int r0 = 0; r0 < c.num_reqs; r0 += 64) {
     const int k = r0 + lane;
@@ -60,56 +59,86 @@ __global__ __launch_bounds__(256) void combine_d128(const CombineParams c) {
     r += n;
     if (n < 64) break;
   }
-  if (r >= c.num_reqs) return;  // a padding row beyond qsl[R]
-  int S = c.num_splits;
-  if (c.seq_lens != nullptr) {
-    const int q_start = c.qsl[r];
-    S = request_splits(c.qsl[r + 1] - q_start, c.seq_lens[r], c.bq, c.window,
-                       c.causal != 0, c.num_splits);
-  }
+  return r;
+}
 
+// The splits the attention kernel wrote for row (tok, head) of request r
+// under the stream partition: their count (live).
+__device__ __forceinline__ int row_live_splits(const CombineParams& c, int r, int64_t tok,
+                                               int head, int lane) {
+  const StreamDesc d{c.qsl, c.seq_lens, c.num_reqs, c.bq, c.window, c.causal, c.n_hg,
+                     c.num_wg, c.num_splits};
+  int64_t total;
+  const int64_t per = stream_per(d, lane, total);
+  const int q_start = ld_ro(c.qsl, r);
+  const int q_len = ld_ro(c.qsl, r + 1) - q_start;
+  const int seq_len = ld_ro(c.seq_lens, r);
+  const int tok_in = static_cast<int>(tok) - q_start;
+  const int j = tok_in / c.bq;
+  const int row = (tok_in - j * c.bq) * c.group + head % c.group;
+  const int hu = (head / c.group) * c.n_rg + row / kRowsPerWave;
+  int64_t at = positions_before(d, r, lane);
+  for (int k = 0; k < j; ++k)
+    at += static_cast<int64_t>(tile_chunks(request_tile(r, q_start, q_len, seq_len, c.bq, k),
+                                           c.window, c.causal != 0)) *
+          c.n_hg;
+  const int32_t n = tile_chunks(request_tile(r, q_start, q_len, seq_len, c.bq, j), c.window,
+                                c.causal != 0);
+  int first, live;
+  stream_splits(at + static_cast<int64_t>(hu / kGroupUnits) * n, n, per, first, live);
+  return live;
+}
+
+// Merges splits of the 64-split blocks first, first + step, ... of row
+// (tok, head): the maximum M of their log2-LSEs and, relative to it, this
+// lane's two numerator columns and the (wave-summed) denominator.
+__device__ __forceinline__ void merge_blocks(const CombineParams& c, int64_t tok, int head, int S,
+                                             int first, int step, int lane, float& M, f32x2& num,
+                                             float& den) {
   const char* lse_row = c.ws_lse + tok * c.s_wl_tok + static_cast<int64_t>(head) * c.s_wl_head;
   const char* o_row = c.ws_o + tok * c.s_wo_tok + static_cast<int64_t>(head) * c.s_wo_head + 8 * lane;
-
-  float M = kNegInf;
-  for (int s = lane; s < S; s += 64) {
+  M = kNegInf;
+  for (int s = 64 * first + lane; s < S; s += 64 * step) {
     const float x = *reinterpret_cast<const float*>(lse_row + s * c.s_wl_split);
     M = x > M ? x : M;  // -inf and NaN never win
   }
   M = wave_max(M);
-  f32x2 num = {0.0f, 0.0f};
-  float den = 0.0f;
-  if (M > kNegInf) {
-    float den_l = 0.0f;
-    for (int s0 = 0; s0 < S; s0 += 64) {
-      const int s = s0 + lane;
-      const float x = s < S ? *reinterpret_cast<const float*>(lse_row + s * c.s_wl_split) : kNegInf;
-      const float w_l = x > kNegInf ? __builtin_amdgcn_exp2f(x - M) : 0.0f;
-      den_l += w_l;
-      const int n = S - s0 < 64 ? S - s0 : 64;
-      for (int e0 = 0; e0 < n; e0 += kBatch) {
-        float w[kBatch];
-        f32x2 ov[kBatch];
+  num = (f32x2){0.0f, 0.0f};
+  den = 0.0f;
+  if (!(M > kNegInf)) return;
+  float den_l = 0.0f;
+  for (int s0 = 64 * first; s0 < S; s0 += 64 * step) {
+    const int s = s0 + lane;
+    const float x = s < S ? *reinterpret_cast<const float*>(lse_row + s * c.s_wl_split) : kNegInf;
+    const float w_l = x > kNegInf ? __builtin_amdgcn_exp2f(x - M) : 0.0f;
+    den_l += w_l;
+    const int n = S - s0 < 64 ? S - s0 : 64;
+    for (int e0 = 0; e0 < n; e0 += kBatch) {
+      float w[kBatch];
+      f32x2 ov[kBatch];
 #pragma unroll
-        for (int k = 0; k < kBatch; ++k) {
-          const int e = e0 + k;
-          w[k] = e < n ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(
-                                                        __builtin_bit_cast(int, w_l), e))
-                       : 0.0f;
-          ov[k] = w[k] > 0.0f ? *reinterpret_cast<const f32x2*>(o_row + (s0 + e) * c.s_wo_split)
-                              : (f32x2){0.0f, 0.0f};
-        }
+      for (int k = 0; k < kBatch; ++k) {
+        const int e = e0 + k;
+        w[k] = e < n ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(
+                                                      __builtin_bit_cast(int, w_l), e))
+                     : 0.0f;
+        ov[k] = w[k] > 0.0f ? *reinterpret_cast<const f32x2*>(o_row + (s0 + e) * c.s_wo_split)
+                            : (f32x2){0.0f, 0.0f};
+      }
 #pragma unroll
-        for (int k = 0; k < kBatch; ++k) {
-          if (w[k] > 0.0f) {
-            num[0] = fmaf(w[k], ov[k][0], num[0]);
-            num[1] = fmaf(w[k], ov[k][1], num[1]);
-          }
+      for (int k = 0; k < kBatch; ++k) {
+        if (w[k] > 0.0f) {
+          num[0] = fmaf(w[k], ov[k][0], num[0]);
+          num[1] = fmaf(w[k], ov[k][1], num[1]);
         }
       }
     }
-    den = wave_sum(den_l);
   }
+  den = wave_sum(den_l);
+}
+
+__device__ __forceinline__ void write_row(const CombineParams& c, int64_t tok, int head, float M,
+                                          f32x2 num, float den, int lane) {
   const float inv = den > 0.0f ? 1.0f / den : 0.0f;
   const float r0 = num[0] * inv, r1 = num[1] * inv;
   char* dst = c.out + tok * c.s_out_tok + static_cast<int64_t>(head) * c.s_out_head;
@@ -127,11 +156,115 @@ __global__ __launch_bounds__(256) void combine_d128(const CombineParams c) {
   }
 }
 
+// Rows with more splits than this are merged by all 4 waves of the
+// work-group together; the others by wave 0 alone.
+constexpr int kSharedRowSplits = 64;
+
+__global__ __launch_bounds__(256) void combine_d128(const CombineParams c) {
+  __shared__ int row_splits;
+  __shared__ float part_m[kWaves], part_den[kWaves];
+  __shared__ f32x2 part_num[kWaves][64];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if (!c.shared_rows) {  // one row per wave, whatever its split count
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * kWaves + wave;
+    const int64_t tok = row / c.num_q_heads;
+    const int head = static_cast<int>(row - tok * c.num_q_heads);
+    if (tok >= c.num_tokens) return;
+    const int r = request_of_token(c, tok, lane);
+    if (r >= c.num_reqs) return;  // a padding row beyond qsl[R]
+    const int S = c.seq_lens != nullptr ? row_live_splits(c, r, tok, head, lane) : c.num_splits;
+    if (c.seq_lens != nullptr && S == 1) return;  // written to out by the attention kernel
+    float M, den;
+    f32x2 num;
+    merge_blocks(c, tok, head, S, 0, 1, lane, M, num, den);
+    write_row(c, tok, head, M, num, den, lane);
+    return;
+  }
+  const int64_t row = blockIdx.x;
+  const int64_t tok = row / c.num_q_heads;
+  const int head = static_cast<int>(row - tok * c.num_q_heads);
+  if (wave == 0) {  // the row's split count (0: nothing to merge)
+    int S = 0;
+    const int r = request_of_token(c, tok, lane);
+    if (r < c.num_reqs) {  // not a padding row beyond qsl[R]
+      S = c.seq_lens != nullptr ? row_live_splits(c, r, tok, head, lane) : c.num_splits;
+      if (c.seq_lens != nullptr && S == 1) S = 0;  // written to out by the attention kernel
+    }
+    if (lane == 0) row_splits = S;
+  }
+  __syncthreads();
+  const int S = row_splits;
+  float M, den;
+  f32x2 num;
+  if (S <= kSharedRowSplits) {
+    if (wave != 0 || S == 0) return;
+    merge_blocks(c, tok, head, S, 0, 1, lane, M, num, den);
+    write_row(c, tok, head, M, num, den, lane);
+    return;
+  }
+  // The 4 waves take the 64-split blocks in turn; wave 0 merges their
+  // results in a fixed order.
+  merge_blocks(c, tok, head, S, wave, kWaves, lane, M, num, den);
+  if (lane == 0) {
+    part_m[wave] = M;
+    part_den[wave] = den;
+  }
+  part_num[wave][lane] = num;
+  __syncthreads();
+  if (wave != 0) return;
+  float Mg = kNegInf;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) Mg = part_m[w] > Mg ? part_m[w] : Mg;
+  f32x2 ng = {0.0f, 0.0f};
+  float dg = 0.0f;
+  if (Mg > kNegInf) {
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      if (part_m[w] > kNegInf) {
+        const float a = __builtin_amdgcn_exp2f(part_m[w] - Mg);
+        const f32x2 pn = part_num[w][lane];
+        ng[0] = fmaf(a, pn[0], ng[0]);
+        ng[1] = fmaf(a, pn[1], ng[1]);
+        dg = fmaf(a, part_den[w], dg);
+      }
+    }
+  }
+  write_row(c, tok, head, Mg, ng, dg, lane);
+}
+
+// -inf into the log2-LSE slot of every split s >= live of every query row
+// (live: the splits the attention kernel wrote for the row), so that a
+// combine over all num_splits splits ignores them, as the reference's launch
+// contract requires of the split partials (reference attn_args.h:38-44). One
+// wave per row; padding rows are not written.
+__global__ __launch_bounds__(256) void fill_unused_splits(const CombineParams c) {
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * kWaves + wave;
+  const int64_t tok = row / c.num_q_heads;
+  const int head = static_cast<int>(row - tok * c.num_q_heads);
+  if (tok >= c.num_tokens) return;
+  const int r = request_of_token(c, tok, lane);
+  if (r >= c.num_reqs) return;
+  const int live = row_live_splits(c, r, tok, head, lane);
+  char* lse_row = const_cast<char*>(c.ws_lse) + tok * c.s_wl_tok + static_cast<int64_t>(head) * c.s_wl_head;
+  for (int s = live + lane; s < c.num_splits; s += 64)
+    *reinterpret_cast<float*>(lse_row + s * c.s_wl_split) = kNegInf;
+}
+
 }  // namespace
+
+hipError_t launch_fill_unused_splits(const CombineParams& c, hipStream_t stream) {
+  const int64_t rows = static_cast<int64_t>(c.num_tokens) * c.num_q_heads;
+  const unsigned blocks = static_cast<unsigned>((rows + kWaves - 1) / kWaves);
+  hipLaunchKernelGGL(fill_unused_splits, dim3(blocks), dim3(kWaves * 64), 0, stream, c);
+  return hipGetLastError();
+}
 
 hipError_t launch_combine_kernel(const CombineParams& c, hipStream_t stream) {
   const int64_t rows = static_cast<int64_t>(c.num_tokens) * c.num_q_heads;
-  const unsigned blocks = static_cast<unsigned>((rows + kWaves - 1) / kWaves);
+  const unsigned blocks = static_cast<unsigned>(c.shared_rows ? rows : (rows + kWaves - 1) / kWaves);
   hipLaunchKernelGGL(combine_d128, dim3(blocks), dim3(kWaves * 64), 0, stream, c);
   return hipGetLastError();
 }

@@ -43,7 +43,7 @@
 // max is reduced over the 4 lanes of a row with two xor shuffles; the
 // running sum stays per lane and is reduced once at the end.
 
-#include "attn_internal.h"
+#include "attn_stream.h"
 
 #ifndef PA_PAGED_INFLIGHT
 #define PA_PAGED_INFLIGHT 2
@@ -146,7 +146,7 @@ struct Chunk {
 // Waves per work-group of the attention kernel: one per KV head of a decode
 // tile, so the 8 cells of a token (8 x 264 contiguous bytes for NHD pages)
 // are read by one CU.
-constexpr int kFwdWaves = 8;
+constexpr int kFwdWaves = kGroupUnits;
 // LDS staging of the paged path: two 32-key chunk slots per wave, each
 // [K: 32 x 128 B | V: 32 x 128 B | k_scale x 32, v_scale x 32].
 constexpr int kSlotK = 0;
@@ -155,6 +155,8 @@ constexpr int kSlotScale = 8192;
 constexpr int kSlotBytes = 8192 + 256;
 // Direct-to-LDS loads of one chunk: 4 for K, 4 for V, 1 for the scales.
 constexpr int kDmaPerChunk = 9;
+// Chunks between the waves' rendezvous in the paged kernel.
+constexpr int kRealignChunks = 32;
 
 // s_waitcnt with only the vector-memory counter (<= n outstanding) or only
 // the LDS counter (0 outstanding). Inline asm with a memory clobber, so the
@@ -198,67 +200,9 @@ __device__ __forceinline__ const char* at(const CacheStream& s, int64_t page,
          static_cast<int64_t>(head) * s.s_head;
 }
 
-// One work unit: rows [16 rg, 16 rg + 16) of row tile t, KV head kvh, split
-// Read-only inputs (query_start_loc, seq_lens, block_table) are read through
-// the constant address space: a wave-uniform index then becomes a scalar
-// load, which is tracked by lgkmcnt and never makes the wave wait for its
-// vector loads in flight.
-__device__ __forceinline__ int32_t ld_ro(const int32_t* base, int64_t i) {
-  return ((const int32_t __attribute__((address_space(4)))*)(base))[i];
-}
-
-// Cursor over the unit table of one wave: the current 64-request chunk, with
-// the inclusive prefix of units per lane. Units are requested in increasing
-// order, so the cursor only moves forward.
-struct Cursor {
-  int r0 = -64;  // first request of the chunk
-  int u0 = 0;    // units before the chunk
-  int u1 = 0;    // units through the chunk
-  int incl = 0;  // per lane: inclusive prefix within the chunk
-  bool end = false;
-};
-
-// Finds unit u (>= every unit asked before on this cursor). False when u is
-// past the table. On success req is the request and u_loc the unit's index
-// within the request.
-template <bool kWindow>
-__device__ __forceinline__ bool find_unit(const AttnParams& p, Cursor& cu, int u, int lane,
-                                          int& req, int& u_loc) {
-  const int window = kWindow ? p.window : 0;
-  const bool causal = kWindow ? (p.causal != 0) : true;
-  while (!cu.end && u >= cu.u1) {
-    cu.r0 += 64;
-    cu.u0 = cu.u1;
-    if (cu.r0 >= p.num_reqs) {
-      cu.end = true;
-      break;
-    }
-    const int r = cu.r0 + lane;
-    int units = 0;
-    if (r < p.num_reqs) {
-      const int ql = p.qsl[r + 1] - p.qsl[r];
-      units = request_row_tiles(ql, p.bq) *
-              request_splits(ql, p.seq_lens[r], p.bq, window, causal, p.num_splits) * p.n_hu;
-    }
-    int incl = units;
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-      const int v = __shfl_up(incl, d);
-      if (lane >= d) incl += v;
-    }
-    cu.incl = incl;
-    cu.u1 = cu.u0 + __builtin_amdgcn_readlane(incl, 63);
-  }
-  if (cu.end) return false;
-  const int local = u - cu.u0;
-  const int j = static_cast<int>(__popcll(__ballot(cu.incl <= local)));
-  const int excl = j > 0 ? __builtin_amdgcn_readlane(cu.incl, j - 1) : 0;
-  req = cu.r0 + j;
-  u_loc = local - excl;
-  return true;
-}
-
-// Everything about one work unit that is uniform across the wave.
+// Everything about one work unit that is uniform across the wave: rows
+// [16 rg, 16 rg + 16) of row tile t, KV head kvh, the keys [c_lo, c_hi) of
+// split s of the row tile's stream (live splits in all).
 struct Unit {
   RowTile t;
   int s, live, kvh, rg;
@@ -271,18 +215,16 @@ struct Unit {
   int w_lo_max, w_hi_min;  // a chunk outside [w_lo_max, w_hi_min] needs the mask
 };
 
+// Unit of KV-head unit hu (= kvh * row groups + rg) of row tile t over the
+// keys [c_lo, c_hi) (c_lo 32-aligned), trimmed to the keys its rows see.
 template <bool kWindow>
-__device__ __forceinline__ void make_unit(const AttnParams& p, int req, int u_loc, Unit& U) {
+__device__ __forceinline__ void make_unit(const AttnParams& p, const RowTile& t, int hu,
+                                          int c_lo, int c_hi, int s, int live, Unit& U) {
   const int window = kWindow ? p.window : 0;
   const bool causal = kWindow ? (p.causal != 0) : true;
-  const int q_start = ld_ro(p.qsl, req);
-  const int q_len = ld_ro(p.qsl, req + 1) - q_start;
-  const int seq_len = ld_ro(p.seq_lens, req);
-  U.live = request_splits(q_len, seq_len, p.bq, window, causal, p.num_splits);
-  const int hu = u_loc % p.n_hu;
-  const int t2 = u_loc / p.n_hu;
-  U.s = t2 % U.live;
-  U.t = request_tile(req, q_start, q_len, seq_len, p.bq, t2 / U.live);
+  U.t = t;
+  U.s = s;
+  U.live = live;
   U.kvh = static_cast<int>(p.rg_div.div(hu));
   U.rg = hu - U.kvh * static_cast<int>(p.rg_div.d);
   const int G = p.group;
@@ -298,19 +240,114 @@ __device__ __forceinline__ void make_unit(const AttnParams& p, int req, int u_lo
   U.w_lo_max = key_lo(U.t, tok_last, window);
   U.w_hi_min = key_hi(U.t, tok_first, window, causal);
   const int w_hi_max = key_hi(U.t, tok_last, window, causal);
-  // The row tile's KV tiles, cut into the request's live splits.
-  const int rbeg = kWindow ? range_begin(U.t, window) : 0;
-  const int rend = range_end(U.t, window, causal);
-  const int ft = first_kv_tile(rbeg);
-  const int nt = kv_tile_count(rbeg, rend);
-  int tb, te;
-  split_range(U.s, U.live, nt, tb, te);
-  const int c_lo = (ft + tb) * kTileTokens, c_hi = (ft + te) * kTileTokens;
   U.ld_lo = c_lo > w_lo_min ? c_lo : w_lo_min;
   U.ld_hi = c_hi < w_hi_max + 1 ? c_hi : w_hi_max + 1;
   U.c_begin = U.ld_lo & ~(kChunkTokens - 1);
   U.n_chunks = U.c_begin < U.ld_hi ? (U.ld_hi - U.c_begin + kChunkTokens - 1) / kChunkTokens : 0;
 }
+
+// The work of one wave, in the order it runs it. Two partitions:
+//   * num_splits == 1: units are (request, row tile, KV-head unit), whole
+//     key ranges; wave w of the grid's W waves takes units w, w + W, ...,
+//     of a table derived on the device from query_start_loc and seq_lens
+//     (a prefix sum over requests, 64 per wave instruction).
+//   * num_splits > 1 (kStream): the chunk-stream partition of
+//     attn_geometry.h. Work-group b runs positions [b per, (b + 1) per);
+//     wave w of it takes KV-head unit 8 g + w of each group g it meets, so
+//     the 8 waves of a work-group read the 8 adjacent heads of the same keys
+//     (their cells share cache lines), and every split but a stream's last
+//     is exactly per chunks long.
+template <bool kWindow, bool kStream>
+struct Work {
+  // num_splits == 1
+  int r0 = -64;  // first request of the cursor's 64-request window
+  int u0 = 0;    // units before the window
+  int u1 = 0;    // units through the window
+  int incl = 0;  // per lane: inclusive prefix within the window
+  int next_u = 0;
+  int stride = 0;
+  // num_splits > 1
+  StreamCursor sc;
+  StreamDesc d;
+  int64_t pos = 0, stop = 0, per = 1;
+  int wg = 0, wave = 0;
+
+  __device__ __forceinline__ void init(const AttnParams& p, int lane) {
+    const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
+    if constexpr (kStream) {
+      d = StreamDesc{p.qsl, p.seq_lens, p.num_reqs, p.bq, kWindow ? p.window : 0,
+                     kWindow ? p.causal : 1, p.n_hg, static_cast<int32_t>(gridDim.x),
+                     p.num_splits};
+      int64_t total;
+      per = stream_per(d, lane, total);
+      wg = blockIdx.x;
+      wave = w;
+      pos = static_cast<int64_t>(wg) * per;
+      stop = pos + per < total ? pos + per : total;
+    } else {
+      next_u = blockIdx.x * kGroupUnits + w;
+      stride = gridDim.x * kGroupUnits;
+    }
+  }
+
+  // The next unit of this wave (possibly without rows or keys); false at the
+  // end of its work.
+  __device__ __forceinline__ bool next(const AttnParams& p, int lane, Unit& U) {
+    if constexpr (kStream) {
+      while (pos < stop) {
+        StreamPos sp;
+        if (!stream_locate(d, sc, pos, lane, sp)) {
+          pos = stop;
+          return false;
+        }
+        const int c0 = static_cast<int>(pos - sp.c0);
+        const int64_t end = sp.c0 + sp.n < stop ? sp.c0 + sp.n : stop;
+        const int c1 = static_cast<int>(end - sp.c0);
+        pos = end;
+        const int hu = sp.hg * kGroupUnits + wave;
+        if (hu >= p.n_hu) continue;  // the group has fewer units than waves
+        int first, live;
+        stream_splits(sp.c0, sp.n, per, first, live);
+        make_unit<kWindow>(p, sp.t, hu, sp.cb + kChunkTokens * c0, sp.cb + kChunkTokens * c1,
+                           wg - first, live, U);
+        return true;
+      }
+      return false;
+    } else {
+      const int window = kWindow ? p.window : 0;
+      const bool causal = kWindow ? (p.causal != 0) : true;
+      const int u = next_u;
+      next_u += stride;
+      while (u >= u1) {
+        r0 += 64;
+        u0 = u1;
+        if (r0 >= p.num_reqs) return false;
+        const int r = r0 + lane;
+        const int units =
+            r < p.num_reqs ? request_row_tiles(p.qsl[r + 1] - p.qsl[r], p.bq) * p.n_hu : 0;
+        int x = units;
+#pragma unroll
+        for (int dd = 1; dd < 64; dd <<= 1) {
+          const int v = __shfl_up(x, dd);
+          if (lane >= dd) x += v;
+        }
+        incl = x;
+        u1 = u0 + __builtin_amdgcn_readlane(x, 63);
+      }
+      const int local = u - u0;
+      const int j = static_cast<int>(__popcll(__ballot(incl <= local)));
+      const int req = r0 + j;
+      const int u_loc = local - (j > 0 ? __builtin_amdgcn_readlane(incl, j - 1) : 0);
+      const int q_start = ld_ro(p.qsl, req);
+      const int q_len = ld_ro(p.qsl, req + 1) - q_start;
+      const int seq_len = ld_ro(p.seq_lens, req);
+      const RowTile t = request_tile(req, q_start, q_len, seq_len, p.bq, u_loc / p.n_hu);
+      make_unit<kWindow>(p, t, u_loc % p.n_hu, tile_chunk_base(t, window),
+                         range_end(t, window, causal), 0, 1, U);
+      return true;
+    }
+  }
+};
 
 // Per-lane view of the unit's rows: lane l holds row row0 + (l % 16).
 struct Lanes {
@@ -511,7 +548,7 @@ struct Finished {
   int64_t qtok;
   int head, g;
   bool vrow;
-  int s;
+  int s, live;
 };
 
 __device__ __forceinline__ void finish(const Unit& U, const Lanes& L, const State& st,
@@ -528,25 +565,32 @@ __device__ __forceinline__ void finish(const Unit& U, const Lanes& L, const Stat
   f.g = L.g;
   f.vrow = L.vrow;
   f.s = U.s;
+  f.live = U.live;
 }
 
-// Stores a finished unit: out (S == 1) or the split partials (S > 1). The
-// split slots [live, S) that a request does not use are left untouched here
-// (fill_unused_splits writes them when a caller needs them).
-// Vector memory instructions store_finished issues per unit, the same for
-// every unit of a launch (the lanes without a row are masked off, never the
-// whole wave: row 0 of a unit always exists), so that the waits of the chunk
+// Whether a finished unit goes to out (num_splits == 1, or a single-split
+// stream when the launch writes those directly) or to the split partials.
+__device__ __forceinline__ bool direct_out(const AttnParams& p, int live) {
+  return p.num_splits == 1 || (live == 1 && p.direct_single != 0);
+}
+
+// Vector memory instructions store_finished issues for a unit, known before
+// it is issued (the lanes without a row are masked off, never the whole
+// wave: row 0 of a unit always exists), so that the waits of the chunk
 // pipeline can count past them.
-__device__ __forceinline__ int stores_per_unit(const AttnParams& p) {
-  if (p.num_splits > 1) return 9;
+__device__ __forceinline__ int stores_per_unit(const AttnParams& p, int live) {
+  if (!direct_out(p, live)) return 9;
   return (p.out_dtype == PTH_ATTN_F32 ? 8 : 4) + (p.lse_out != nullptr ? 1 : 0);
 }
 
+// Stores a finished unit: out (and lse_out, natural log) or its split's
+// partials. Split slots a row does not use are left untouched here
+// (fill_unused_splits writes them when a caller needs them).
 __device__ __forceinline__ void store_finished(const AttnParams& p, const Finished& f) {
   if (!f.vrow) return;
   const int g = f.g;
   const int64_t head = f.head;
-  if (p.num_splits > 1) {
+  if (!direct_out(p, f.live)) {
     char* dst = reinterpret_cast<char*>(p.ws_o) + f.s * p.s_wo_split + f.qtok * p.s_wo_tok +
                 head * p.s_wo_head + 4 * 32 * g;
 #pragma unroll
@@ -610,9 +654,9 @@ __device__ __forceinline__ void epilogue(const AttnParams& p, const Unit& U, con
 // chunk before them from registers. The producer crosses unit boundaries, so
 // a new unit's first chunks are already in flight while the previous unit
 // finishes: the pipeline does not drain between units.
+template <bool kWindow, bool kStream>
 struct Producer {
-  Cursor cur;
-  int next_u;
+  Work<kWindow, kStream> work;
   Unit U;
   int k;  // next chunk of U to issue
   bool done;
@@ -626,7 +670,8 @@ struct Producer {
 };
 
 // The per-lane offsets of unit U's KV head.
-__device__ __forceinline__ void producer_offsets(const AttnParams& p, Producer& P, int lane) {
+template <class Prod>
+__device__ __forceinline__ void producer_offsets(const AttnParams& p, Prod& P, int lane) {
   const uint32_t kq = lane >> 3, piece = lane & 7;
   const uint32_t head = static_cast<uint32_t>(P.U.kvh) * p.cell_head;
   const uint32_t sw = 16u * (piece ^ kq);  // row r's piece c goes to LDS position c ^ (r & 7)
@@ -642,7 +687,8 @@ __device__ __forceinline__ void producer_offsets(const AttnParams& p, Producer& 
 
 // Block-table lookup for chunk k of the producer's unit (scalar loads; a
 // 16-key group outside the unit's keys reads page 0 and is masked later).
-__device__ __forceinline__ void producer_pages(const AttnParams& p, Producer& P) {
+template <class Prod>
+__device__ __forceinline__ void producer_pages(const AttnParams& p, Prod& P) {
   const Unit& U = P.U;
   const int c = U.c_begin + kChunkTokens * P.k;
   const int64_t bt0 = static_cast<int64_t>(U.t.req) * p.bt_stride;
@@ -660,17 +706,13 @@ __device__ __forceinline__ void producer_pages(const AttnParams& p, Producer& P)
 }
 
 // Moves the producer to its next chunk; false when the wave has no more.
-template <bool kWindow>
-__device__ __forceinline__ bool producer_next(const AttnParams& p, Producer& P, int lane,
-                                              int num_workers) {
+template <class Prod>
+__device__ __forceinline__ bool producer_next(const AttnParams& p, Prod& P, int lane) {
   while (!P.done && P.k >= P.U.n_chunks) {
-    int req, u_loc;
-    if (!find_unit<kWindow>(p, P.cur, P.next_u, lane, req, u_loc)) {
+    if (!P.work.next(p, lane, P.U)) {
       P.done = true;
       break;
     }
-    P.next_u += num_workers;
-    make_unit<kWindow>(p, req, u_loc, P.U);
     P.k = 0;
     if (P.U.n_chunks > 0) {
       producer_offsets(p, P, lane);
@@ -688,7 +730,8 @@ __device__ __forceinline__ bool producer_next(const AttnParams& p, Producer& P, 
 // cache: a key outside the unit's range reads another slot of the same page
 // (or of page 0) and is masked by the consumer, so every chunk issues
 // exactly kDmaPerChunk loads.
-__device__ __forceinline__ void issue_chunk(const AttnParams& p, Producer& P, char* slot, int lane) {
+template <class Prod>
+__device__ __forceinline__ void issue_chunk(const AttnParams& p, Prod& P, char* slot, int lane) {
   const char* base[2];
 #pragma unroll
   for (int sub = 0; sub < 2; ++sub)
@@ -788,19 +831,29 @@ __device__ __forceinline__ void read_chunk(uint32_t base, const ReadOffsets& o, 
 // outside the listed ones fall back to a full wait.
 __device__ __forceinline__ void wait_vmcnt_dyn(int younger) {
   switch (younger) {
+    case 1: wait_vmcnt<1>(); break;
+    case 2: wait_vmcnt<2>(); break;
+    case 3: wait_vmcnt<3>(); break;
     case 4: wait_vmcnt<4>(); break;
     case 5: wait_vmcnt<5>(); break;
+    case 6: wait_vmcnt<6>(); break;
+    case 7: wait_vmcnt<7>(); break;
     case 8: wait_vmcnt<8>(); break;
     case 9: wait_vmcnt<9>(); break;
+    case 10: wait_vmcnt<10>(); break;
+    case 11: wait_vmcnt<11>(); break;
+    case 12: wait_vmcnt<12>(); break;
     case 13: wait_vmcnt<13>(); break;
     case 14: wait_vmcnt<14>(); break;
+    case 15: wait_vmcnt<15>(); break;
+    case 16: wait_vmcnt<16>(); break;
     case 17: wait_vmcnt<17>(); break;
     case 18: wait_vmcnt<18>(); break;
     default: wait_vmcnt<0>(); break;
   }
 }
 
-template <bool kWindow, bool kF16Q, int kInFlight>
+template <bool kWindow, bool kStream, bool kF16Q, int kInFlight>
 __global__ __launch_bounds__(kFwdWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void attn_fwd_paged(const AttnParams p) {
   __shared__ __attribute__((aligned(16))) char lds_all[kFwdWaves * kInFlight * kSlotBytes];
@@ -810,11 +863,9 @@ void attn_fwd_paged(const AttnParams p) {
   const uint32_t lds_base = lds_offset(lds);
   const ReadOffsets ro = read_offsets(lane);
   const float scl = scale_factor(lane & 15, p.scale_log2);
-  const int worker = blockIdx.x * kFwdWaves + wave;
-  const int num_workers = gridDim.x * kFwdWaves;
 
-  Producer P;
-  P.next_u = worker;
+  Producer<kWindow, kStream> P;
+  P.work.init(p, lane);
   P.U.n_chunks = 0;
   P.k = 0;
   P.done = false;
@@ -822,15 +873,15 @@ void attn_fwd_paged(const AttnParams p) {
   int slot_w = 0;    // slot the producer fills next
 #pragma unroll
   for (int i = 0; i < kInFlight; ++i) {
-    if (producer_next<kWindow>(p, P, lane, num_workers)) {
+    if (producer_next(p, P, lane)) {
       issue_chunk(p, P, lds + slot_w * kSlotBytes, lane);
       ++inflight;
       slot_w = slot_w + 1 == kInFlight ? 0 : slot_w + 1;
     }
   }
 
-  Cursor cur;
-  int next_u = worker;
+  Work<kWindow, kStream> work;  // the consumer's walk: the same units, behind
+  work.init(p, lane);
   Unit U;
   Lanes L;
   State st;
@@ -843,7 +894,7 @@ void attn_fwd_paged(const AttnParams p) {
   // order, so a store issued in front of chunks still in flight would make
   // every wait for those chunks wait for the store as well. The waits of
   // the chunks that were in flight before the stores count past them.
-  const int n_store = stores_per_unit(p);
+  int n_store = 0;
   int older_than_stores = 0;  // chunks in flight issued before the last stores
   while (true) {
     if (!have || ck >= U.n_chunks) {
@@ -851,10 +902,7 @@ void attn_fwd_paged(const AttnParams p) {
       const bool had = have;
       if (have) finish(U, L, st, done);
       have = false;
-      int req, u_loc;
-      while (find_unit<kWindow>(p, cur, next_u, lane, req, u_loc)) {
-        next_u += num_workers;
-        make_unit<kWindow>(p, req, u_loc, U);
+      while (work.next(p, lane, U)) {
         if (!U.has_rows) continue;
         L = unit_lanes<kWindow>(p, U, lane);
         if (U.n_chunks == 0) {  // no key of these rows in this split
@@ -873,6 +921,7 @@ void attn_fwd_paged(const AttnParams p) {
       __builtin_amdgcn_s_waitcnt(0x0F70);
       if (had) {
         store_finished(p, done);
+        n_store = stores_per_unit(p, done.live);
         older_than_stores = inflight;
       }
       if (!have) break;
@@ -889,13 +938,119 @@ void attn_fwd_paged(const AttnParams p) {
     read_chunk(lds_base + slot_r * kSlotBytes, ro, ch);  // returns once the reads landed
     --inflight;
     slot_r = slot_r + 1 == kInFlight ? 0 : slot_r + 1;
-    if (producer_next<kWindow>(p, P, lane, num_workers)) {
+    if (producer_next(p, P, lane)) {
       issue_chunk(p, P, lds + slot_w * kSlotBytes, lane);
       ++inflight;
       slot_w = slot_w + 1 == kInFlight ? 0 : slot_w + 1;
     }
     compute_chunk<kF16Q>(U, L, U.c_begin + kChunkTokens * ck, ch, qb, qlo, scl, st);
+    // Re-align the work-group's waves now and then: they read adjacent cells
+    // whose shared cache lines are fetched once only while the waves stay
+    // close (a wave running far ahead gets them evicted before its
+    // neighbour asks). Only a rendezvous: no data passes through it, and a
+    // wave that has finished its work no longer holds the others.
+    if ((ck & (kRealignChunks - 1)) == kRealignChunks - 1) __builtin_amdgcn_s_barrier();
     ++ck;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Paged kernel with register loads (block size a multiple of 16, cell view of
+// the cache): each lane loads exactly the bytes of its MFMA operands (the
+// layout read_chunk produces from LDS) straight into registers, the next
+// chunk's loads in flight while the current chunk is computed; page numbers
+// are looked up one chunk ahead on the scalar unit.
+struct RegLoader {
+  int32_t page[2], slot0[2];  // pages of the chunk to load next
+  uint32_t off_k, off_v[4], off_s;
+};
+
+__device__ __forceinline__ void reg_offsets(const AttnParams& p, const Unit& U, int lane,
+                                            RegLoader& R) {
+  const uint32_t r16 = lane & 15, g = lane >> 4;
+  const uint32_t head = static_cast<uint32_t>(U.kvh) * p.cell_head;
+  R.off_k = r16 * p.cell_slot + head + 32u * g + p.cell_off[0];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) R.off_v[q] = (4u * g + q) * p.cell_slot + head + p.cell_off[1] + 8u * r16;
+  const uint32_t e = r16 & 7;
+  R.off_s = (4u * g + (e & 3)) * p.cell_slot + head + (r16 < 8 ? p.cell_off[2] : p.cell_off[3]);
+}
+
+__device__ __forceinline__ void reg_pages(const AttnParams& p, const Unit& U, int c,
+                                          RegLoader& R) {
+  const int64_t bt0 = static_cast<int64_t>(U.t.req) * p.bt_stride;
+#pragma unroll
+  for (int sub = 0; sub < 2; ++sub) {
+    const int c16 = c + 16 * sub;
+    R.page[sub] = 0;
+    R.slot0[sub] = 0;
+    if (c16 < U.ld_hi && c16 + 16 > U.ld_lo) {
+      const int blk = static_cast<int>(p.bs_div.div(c16));
+      R.slot0[sub] = c16 - blk * static_cast<int>(p.bs_div.d);
+      R.page[sub] = ld_ro(p.block_table, bt0 + blk);
+    }
+  }
+}
+
+__device__ __forceinline__ void reg_load(const AttnParams& p, const RegLoader& R, int lane,
+                                         Chunk& ch) {
+  const char* base[2];
+#pragma unroll
+  for (int sub = 0; sub < 2; ++sub)
+    base[sub] = p.cell_base +
+                static_cast<uint64_t>(static_cast<uint32_t>(R.page[sub])) * p.cell_block +
+                static_cast<uint32_t>(R.slot0[sub]) * p.cell_slot;
+#pragma unroll
+  for (int sub = 0; sub < 2; ++sub) {
+    ch.k[sub][0] = *reinterpret_cast<const u32x4_a4*>(base[sub] + R.off_k);
+    ch.k[sub][1] = *reinterpret_cast<const u32x4_a4*>(base[sub] + R.off_k + 16);
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) ch.v[e] = *reinterpret_cast<const u32x2_a4*>(base[e >> 2] + R.off_v[e & 3]);
+  const char* sb = ((lane & 7) >> 2) ? base[1] : base[0];
+  ch.sc = *reinterpret_cast<const float*>(sb + R.off_s);
+}
+
+template <bool kWindow, bool kStream, bool kF16Q>
+__global__ __launch_bounds__(kFwdWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void attn_fwd_paged_reg(const AttnParams p) {
+  const int lane = threadIdx.x & 63;
+  const float scl = scale_factor(lane & 15, p.scale_log2);
+  Work<kWindow, kStream> work;
+  work.init(p, lane);
+  Unit U;
+  while (work.next(p, lane, U)) {
+    if (!U.has_rows) continue;
+    const Lanes L = unit_lanes<kWindow>(p, U, lane);
+    State st;
+    state_reset(st);
+    if (U.n_chunks > 0) {
+      RegLoader R;
+      reg_offsets(p, U, lane, R);
+      reg_pages(p, U, U.c_begin, R);
+      Chunk ca, cb;
+      reg_load(p, R, lane, ca);
+      if (U.n_chunks > 1) reg_pages(p, U, U.c_begin + kChunkTokens, R);
+      bf16x8 qb[4], qlo[4];
+      load_q<kF16Q>(p, L, qb, qlo);
+      int k = 0;
+      while (true) {
+        const int c = U.c_begin + kChunkTokens * k;
+        if (k + 1 < U.n_chunks) {
+          reg_load(p, R, lane, cb);
+          if (k + 2 < U.n_chunks) reg_pages(p, U, c + 2 * kChunkTokens, R);
+        }
+        compute_chunk<kF16Q>(U, L, c, ca, qb, qlo, scl, st);
+        if (++k >= U.n_chunks) break;
+        if (k + 1 < U.n_chunks) {
+          reg_load(p, R, lane, ca);
+          if (k + 2 < U.n_chunks) reg_pages(p, U, c + 3 * kChunkTokens, R);
+        }
+        compute_chunk<kF16Q>(U, L, c + kChunkTokens, cb, qb, qlo, scl, st);
+        if (++k >= U.n_chunks) break;
+      }
+    }
+    epilogue(p, U, L, st);
   }
 }
 
@@ -941,20 +1096,15 @@ __device__ __forceinline__ void load_chunk_generic(const AttnParams& p, const Un
   ch.sc = scv;
 }
 
-template <bool kWindow, bool kF16Q>
+template <bool kWindow, bool kStream, bool kF16Q>
 __global__ __launch_bounds__(kFwdWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void attn_fwd_generic(const AttnParams p) {
   const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int worker = blockIdx.x * kFwdWaves + wave;
-  const int num_workers = gridDim.x * kFwdWaves;
   const float scl = scale_factor(lane & 15, p.scale_log2);
-  Cursor cur;
-  for (int u = worker;; u += num_workers) {
-    int req, u_loc;
-    if (!find_unit<kWindow>(p, cur, u, lane, req, u_loc)) break;
-    Unit U;
-    make_unit<kWindow>(p, req, u_loc, U);
+  Work<kWindow, kStream> work;
+  work.init(p, lane);
+  Unit U;
+  while (work.next(p, lane, U)) {
     if (!U.has_rows) continue;
     const Lanes L = unit_lanes<kWindow>(p, U, lane);
     State st;
@@ -982,73 +1132,45 @@ void attn_fwd_generic(const AttnParams p) {
 // Chunks in flight per wave on the paged path (LDS slots per wave).
 constexpr int kPagedInFlight = PA_PAGED_INFLIGHT;
 
-template <bool W, bool F>
+// Windows up to this many keys: the register-load kernel (its short
+// latency wins when every row reads few keys); otherwise the direct-to-LDS
+// pipeline (the higher sustained bandwidth on long rows).
+constexpr int kShortWindow = 4096;
+
+template <bool W, bool St, bool F>
 hipError_t launch_paged(const AttnParams& p, dim3 grid, hipStream_t stream) {
-  hipLaunchKernelGGL((attn_fwd_paged<W, F, kPagedInFlight>), grid, dim3(kFwdWaves * 64), 0,
-                     stream, p);
+  if (W && p.window > 0 && p.window <= kShortWindow) {
+    hipLaunchKernelGGL((attn_fwd_paged_reg<W, St, F>), grid, dim3(kFwdWaves * 64), 0, stream, p);
+  } else {
+    hipLaunchKernelGGL((attn_fwd_paged<W, St, F, kPagedInFlight>), grid, dim3(kFwdWaves * 64), 0,
+                       stream, p);
+  }
   return hipGetLastError();
 }
-template <bool W, bool F>
+template <bool W, bool St, bool F>
 hipError_t launch_generic(const AttnParams& p, dim3 grid, hipStream_t stream) {
-  hipLaunchKernelGGL((attn_fwd_generic<W, F>), grid, dim3(kFwdWaves * 64), 0, stream, p);
+  hipLaunchKernelGGL((attn_fwd_generic<W, St, F>), grid, dim3(kFwdWaves * 64), 0, stream, p);
   return hipGetLastError();
 }
 
-// -inf into the log2-LSE slot of every split s >= live of every query row
-// (live = the splits the row's request uses), so that a combine over all S
-// splits ignores them, as the reference's launch contract requires of the
-// split partials (reference attn_args.h:38-44). One thread per (split,
-// token, head) slot of splits 1..S-1, head fastest: consecutive threads
-// write consecutive floats. Rows of padding tokens are not written.
-__global__ __launch_bounds__(256) void fill_unused_splits(const AttnParams p, int32_t num_tokens,
-                                                          int32_t num_q_heads) {
-  const int64_t per_split = static_cast<int64_t>(num_tokens) * num_q_heads;
-  const int64_t total = per_split * (p.num_splits - 1);
-  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
-       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-    const int s2 = 1 + static_cast<int>(i / per_split);
-    const int64_t r = i - (s2 - 1) * per_split;
-    const int tok = static_cast<int>(r / num_q_heads);
-    const int head = static_cast<int>(r - static_cast<int64_t>(tok) * num_q_heads);
-    if (tok >= p.qsl[p.num_reqs]) continue;
-    int lo = 0, hi = p.num_reqs - 1;  // request: largest r with qsl[r] <= tok
-    while (lo < hi) {
-      const int mid = (lo + hi + 1) >> 1;
-      if (p.qsl[mid] <= tok) lo = mid; else hi = mid - 1;
-    }
-    const int q_start = p.qsl[lo];
-    const int live = request_splits(p.qsl[lo + 1] - q_start, p.seq_lens[lo], p.bq, p.window,
-                                    p.causal != 0, p.num_splits);
-    if (s2 >= live)
-      *reinterpret_cast<float*>(reinterpret_cast<char*>(p.ws_lse) + s2 * p.s_wl_split +
-                                tok * p.s_wl_tok + head * p.s_wl_head) = kNegInf;
-  }
+template <bool W, bool St>
+hipError_t launch_variant(const AttnParams& p, dim3 grid, bool paged16, bool q_f16,
+                          hipStream_t stream) {
+  if (paged16) return q_f16 ? launch_paged<W, St, true>(p, grid, stream)
+                            : launch_paged<W, St, false>(p, grid, stream);
+  return q_f16 ? launch_generic<W, St, true>(p, grid, stream)
+               : launch_generic<W, St, false>(p, grid, stream);
 }
 
 }  // namespace
 
-hipError_t launch_fill_unused_splits(const AttnParams& p, int32_t num_tokens,
-                                     int32_t num_q_heads, hipStream_t stream) {
-  const int64_t total = static_cast<int64_t>(num_tokens) * num_q_heads * (p.num_splits - 1);
-  if (total <= 0) return hipSuccess;
-  const int64_t blocks = (total + 255) / 256;
-  hipLaunchKernelGGL(fill_unused_splits, dim3(static_cast<unsigned>(blocks < 4096 ? blocks : 4096)),
-                     dim3(256), 0, stream, p, num_tokens, num_q_heads);
-  return hipGetLastError();
-}
-
 hipError_t launch_fwd_kernel(const AttnParams& p, dim3 grid, bool windowed,
                              bool paged16, bool q_f16, hipStream_t stream) {
-  if (paged16) {
-    if (windowed) return q_f16 ? launch_paged<true, true>(p, grid, stream)
-                               : launch_paged<true, false>(p, grid, stream);
-    return q_f16 ? launch_paged<false, true>(p, grid, stream)
-                 : launch_paged<false, false>(p, grid, stream);
-  }
-  if (windowed) return q_f16 ? launch_generic<true, true>(p, grid, stream)
-                             : launch_generic<true, false>(p, grid, stream);
-  return q_f16 ? launch_generic<false, true>(p, grid, stream)
-               : launch_generic<false, false>(p, grid, stream);
+  const bool stream_split = p.num_splits > 1;
+  if (windowed) return stream_split ? launch_variant<true, true>(p, grid, paged16, q_f16, stream)
+                                    : launch_variant<true, false>(p, grid, paged16, q_f16, stream);
+  return stream_split ? launch_variant<false, true>(p, grid, paged16, q_f16, stream)
+                      : launch_variant<false, false>(p, grid, paged16, q_f16, stream);
 }
 
 }  // namespace pa

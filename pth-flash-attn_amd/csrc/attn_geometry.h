@@ -9,10 +9,11 @@
 //     of vLLM's unified attention, reference cache_geometry.cuh:336-394);
 //   * the visible key range [lo, hi] of a query token (causal, sliding
 //     window, non-causal; reference cache_geometry.cuh:396-468);
-//   * the KV tiles of a row tile and how they are cut into splits
-//     (reference cache_geometry.cuh:426-432, 506-515), with the MI355X
-//     addition that a row tile uses only as many splits as its length needs
-//     (live_splits below).
+//   * how the keys of all row tiles are cut into splits: an even share of
+//     32-key chunks per work-group (the reference cuts each row tile's KV
+//     tiles into num_splits near-equal ranges, cache_geometry.cuh:426-432,
+//     506-515; here the cut is global, so no work-group idles and short
+//     requests are not split at all).
 // Header-only; needs <stdint.h> only.
 
 #pragma once
@@ -27,19 +28,19 @@
 
 namespace pa {
 
-// KV tokens per tile: the unit of the split partition (the planner's
-// KV_TILE_TOKENS; reference tile_traits.cuh / planner.py:98).
+// KV tokens per tile of the reference's split partition (the planner's
+// KV_TILE_TOKENS; reference tile_traits.cuh / planner.py:98): the unit its
+// window cap on num_splits counts in, reported by pth_attn_tiling.
 constexpr int32_t kTileTokens = 64;
 // KV tokens per softmax step of one wave (two 16-token MFMA column blocks).
 constexpr int32_t kChunkTokens = 32;
 // Query rows per wave: the N of a 16x16x32 MFMA.
 constexpr int32_t kRowsPerWave = 16;
-// Waves per workgroup.
+// Waves per work-group of the combine kernel.
 constexpr int32_t kWaves = 4;
-// A row tile uses no more splits than ceil(tiles / kMinTilesPerSplit): a
-// split shorter than this costs more in prologue and combine than it gains
-// in parallelism. The extra splits of the grid exit at once with lse = -inf.
-constexpr int32_t kMinTilesPerSplit = 4;
+// Waves per work-group of the attention kernel: the KV-head units of one
+// stream group, one per wave.
+constexpr int32_t kGroupUnits = 8;
 
 PA_HD uint32_t mulhi32(uint32_t a, uint32_t b) {
 #if defined(__HIP_DEVICE_COMPILE__)
@@ -150,22 +151,6 @@ PA_HD int32_t range_end(const RowTile& t, int32_t window, bool causal) {
   return key_hi(t, t.tok_begin + t.num_tok - 1, window, causal) + 1;
 }
 
-// KV tiles of the row tile: [first, first + count).
-PA_HD int32_t first_kv_tile(int32_t rbegin) { return rbegin / kTileTokens; }
-PA_HD int32_t kv_tile_count(int32_t rbegin, int32_t rend) {
-  return (rend + kTileTokens - 1) / kTileTokens - first_kv_tile(rbegin);
-}
-
-// Splits a row tile with `count` KV tiles actually uses, out of the grid's
-// num_splits: never more than count / kMinTilesPerSplit (rounded up), never
-// fewer than 1. Read on the device from the device-side lengths, so a
-// captured graph stays valid for any length.
-PA_HD int32_t live_splits(int32_t count, int32_t num_splits) {
-  int32_t want = (count + kMinTilesPerSplit - 1) / kMinTilesPerSplit;
-  if (want < 1) want = 1;
-  return want < num_splits ? want : num_splits;
-}
-
 // Row tile j (0-based) of a request: query tokens [j bq, min((j + 1) bq, q_len)).
 PA_HD RowTile request_tile(int32_t req, int32_t q_start, int32_t q_len,
                            int32_t seq_len, int32_t bq, int32_t j) {
@@ -185,28 +170,61 @@ PA_HD int32_t request_row_tiles(int32_t q_len, int32_t bq) {
   return (q_len + bq - 1) / bq;
 }
 
-// Splits every row tile of a request uses: the live split count of its last
-// row tile, whose key range is the widest (it ends at seq_len; with a window
-// every tile sees about the same number of keys). One count per request keeps
-// the device-side work table a prefix sum over requests.
-PA_HD int32_t request_splits(int32_t q_len, int32_t seq_len, int32_t bq,
-                             int32_t window, bool causal, int32_t num_splits) {
-  if (q_len <= 0) return 0;
-  const RowTile t = request_tile(0, 0, q_len, seq_len, bq,
-                                 request_row_tiles(q_len, bq) - 1);
+// ---------------------------------------------------------------------------
+// Split partition (num_splits > 1). The keys of every row tile, from a
+// 32-aligned base, are a stream of 32-key chunks; the streams of all
+// (request, row tile, group of 8 KV-head units) are laid end to end, in that
+// order, and work-group b of the grid takes positions [b per, (b + 1) per).
+// A stream cut by such a boundary is computed in parts (its splits), one per
+// work-group it meets, and merged by the LSE combine. Every work-group thus
+// gets the same number of chunks, and a stream only has as many splits as
+// the work-groups its length needs.
+
+// First key of chunk 0 of a row tile, and the number of chunks that cover the
+// keys any of its rows sees.
+PA_HD int32_t tile_chunk_base(const RowTile& t, int32_t window) {
   const int32_t rb = window > 0 ? range_begin(t, window) : 0;
+  return rb & ~(kChunkTokens - 1);
+}
+PA_HD int32_t tile_chunks(const RowTile& t, int32_t window, bool causal) {
+  const int32_t base = tile_chunk_base(t, window);
   const int32_t re = range_end(t, window, causal);
-  return live_splits(kv_tile_count(rb, re), num_splits);
+  return re > base ? (re - base + kChunkTokens - 1) / kChunkTokens : 0;
 }
 
-// Tiles [begin, end) (relative to the first tile) of split s < live:
-// [floor(s n / live), floor((s + 1) n / live)); any two differ by at most one
-// tile and they partition [0, n) (reference cache_geometry.cuh:426-432 with
-// the live split count in place of the grid's).
-PA_HD void split_range(int32_t s, int32_t live, int32_t count, int32_t& begin,
-                       int32_t& end) {
-  begin = static_cast<int32_t>(static_cast<int64_t>(s) * count / live);
-  end = static_cast<int32_t>(static_cast<int64_t>(s + 1) * count / live);
+// Sum and maximum of tile_chunks over the row tiles of a request.
+PA_HD void request_chunks(int32_t q_len, int32_t seq_len, int32_t bq, int32_t window,
+                          bool causal, int32_t& sum, int32_t& max) {
+  sum = 0;
+  max = 0;
+  const int32_t tiles = request_row_tiles(q_len, bq);
+  for (int32_t j = 0; j < tiles; ++j) {
+    const int32_t n = tile_chunks(request_tile(0, 0, q_len, seq_len, bq, j), window, causal);
+    sum += n;
+    max = n > max ? n : max;
+  }
+}
+
+// Stream positions per work-group: an even share of `total`, but at least
+// kMinChunksPerSplit and enough that no stream of up to `max_n` chunks
+// meets more than num_splits work-groups (a stream of n chunks meets at most
+// ceil((n - 1) / per) + 1 of them).
+constexpr int32_t kMinChunksPerSplit = 4;
+PA_HD int64_t chunks_per_group(int64_t total, int32_t max_n, int32_t num_wg, int32_t num_splits) {
+  int64_t per = (total + num_wg - 1) / num_wg;
+  if (per < kMinChunksPerSplit) per = kMinChunksPerSplit;
+  if (num_splits > 1 && max_n > 1) {
+    const int64_t need = (static_cast<int64_t>(max_n) - 1 + num_splits - 2) / (num_splits - 1);
+    if (per < need) per = need;
+  }
+  return per;
+}
+
+// The work-groups a stream [c0, c0 + n) meets: first and count (its splits);
+// split s of the stream is work-group first + s.
+PA_HD void stream_splits(int64_t c0, int32_t n, int64_t per, int32_t& first, int32_t& live) {
+  first = static_cast<int32_t>(c0 / per);
+  live = n > 0 ? static_cast<int32_t>((c0 + n - 1) / per) - first + 1 : 1;
 }
 
 }  // namespace pa

@@ -52,13 +52,18 @@ struct AttnParams {
   Div32 bq_div;  // query tokens per row tile
   Div32 rg_div;  // 16-row groups per row tile
   int32_t num_reqs;
-  int32_t n_hu;  // work units per (row tile, split): num_kv_heads * row groups
+  int32_t n_hu;  // KV-head units per row tile: num_kv_heads * row groups
+  int32_t n_hg;  // groups of kGroupUnits KV-head units: ceil(n_hu / 8)
   int32_t bq;    // query tokens per row tile
   int32_t group;
   int32_t num_splits;
   int32_t window;
   int32_t causal;
   int32_t out_dtype;
+  // num_splits > 1: a row whose stream has a single split is written to out
+  // (and lse_out) by the attention kernel itself, and the combine skips it.
+  // Off when the caller combines all num_splits splits itself.
+  int32_t direct_single;
   float scale_log2;  // softmax_scale * log2(e)
 };
 
@@ -78,12 +83,22 @@ struct CombineParams {
   int32_t num_q_heads;
   int32_t num_splits;
   // When seq_lens is non-NULL the combine reads only the splits the
-  // attention kernel used for the row's request (request_splits with these
-  // bq / window / causal); otherwise all num_splits.
+  // attention kernel wrote for the row (the stream partition of
+  // attn_geometry.h for these lengths and launch constants) and skips rows
+  // with a single split, which the attention kernel wrote to out itself;
+  // otherwise it reads all num_splits for every row.
   const int32_t* seq_lens;
   int32_t bq;
+  int32_t group;
+  int32_t n_rg;
+  int32_t n_hg;
+  int32_t num_wg;
   int32_t window;
   int32_t causal;
+  // A work-group per row (rows with many splits are merged by 4 waves)
+  // instead of a wave per row: set when the launch may have more than 64
+  // splits per row and has few rows.
+  int32_t shared_rows;
 };
 
 // Host launchers. They check their arguments, enqueue on `stream`, allocate
@@ -101,15 +116,12 @@ int32_t launch_combine(const PthAttnCombineArgs& c, hipStream_t stream,
                        int64_t lse_stride_head, const PthAttnArgs* split_source);
 
 // Per-variant kernel launches (attn_fwd.hip, attn_combine.hip).
-// Waves per work-group of the attention kernel, and the work-groups that
-// fill the device once (one per CU).
-constexpr int32_t kFwdWavesPerGroup = 8;
+// Work-groups (of kGroupUnits waves) that fill the device once: one per CU.
 int32_t resident_workgroups();
 hipError_t launch_fwd_kernel(const AttnParams& p, dim3 grid, bool windowed,
                              bool paged16, bool q_f16, hipStream_t stream);
 hipError_t launch_combine_kernel(const CombineParams& c, hipStream_t stream);
-hipError_t launch_fill_unused_splits(const AttnParams& p, int32_t num_tokens,
-                                     int32_t num_q_heads, hipStream_t stream);
+hipError_t launch_fill_unused_splits(const CombineParams& c, hipStream_t stream);
 
 const char* last_error();
 int32_t fail(int32_t code, const std::string& msg);

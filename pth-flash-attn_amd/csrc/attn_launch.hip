@@ -101,6 +101,23 @@ int32_t fail(int32_t code, const std::string& msg) {
 }
 void clear_error() { g_last_error.clear(); }
 
+// Launch constants of the split partition of an attention launch (they must
+// be the same in the attention kernel, the combine and the unused-split
+// fill): 16-row groups per row tile, groups of kGroupUnits KV-head units, and
+// the attention grid (one work-group per CU).
+void stream_fields(const PthAttnArgs& a, CombineParams& c) {
+  const int32_t group = a.num_q_heads / a.num_kv_heads;
+  const int32_t rows = a.bq * group;
+  c.seq_lens = a.seq_lens;
+  c.bq = a.bq;
+  c.group = group;
+  c.n_rg = (rows + kRowsPerWave - 1) / kRowsPerWave;
+  c.n_hg = (a.num_kv_heads * c.n_rg + kGroupUnits - 1) / kGroupUnits;
+  c.num_wg = resident_workgroups();
+  c.window = a.window;
+  c.causal = a.causal;
+}
+
 int32_t launch_attention(const PthAttnArgs& a, int32_t loader,
                          hipStream_t stream, float* lse_out,
                          int64_t lse_stride_token, int64_t lse_stride_head,
@@ -191,7 +208,7 @@ int32_t launch_attention(const PthAttnArgs& a, int32_t loader,
   p.s_wl_split = a.ws_lse_stride_split;
   p.s_wl_tok = a.ws_lse_stride_token;
   p.s_wl_head = a.ws_lse_stride_head;
-  p.lse_out = a.num_splits == 1 ? lse_out : nullptr;
+  p.lse_out = lse_out;
   p.s_lo_tok = lse_stride_token;
   p.s_lo_head = lse_stride_head;
   p.k = cache_stream(a.k_cache);
@@ -209,26 +226,33 @@ int32_t launch_attention(const PthAttnArgs& a, int32_t loader,
   p.rg_div = Div32::make(static_cast<uint32_t>(n_rg));
   p.num_reqs = a.num_reqs;
   p.n_hu = a.num_kv_heads * n_rg;
+  p.n_hg = (p.n_hu + kGroupUnits - 1) / kGroupUnits;
   p.bq = a.bq;
   p.group = group;
   p.num_splits = a.num_splits;
   p.window = a.window;
   p.causal = a.causal;
   p.out_dtype = a.out_dtype;
+  p.direct_single = fill_unused_splits ? 0 : 1;
   p.scale_log2 = a.softmax_scale * kLog2e;
 
-  // Persistent grid: one wave per resident slot, but never more waves than
-  // the unit table can hold (sum over requests of row tiles x S x units is
-  // at most (T / bq + R) x S x n_hu).
-  const int64_t tile_bound =
-      a.num_q_tiles > 0 ? a.num_q_tiles
-                        : static_cast<int64_t>(a.num_tokens) / a.bq + a.num_reqs;
-  const int64_t unit_bound = tile_bound * a.num_splits * p.n_hu;
-  const int64_t wg_need = (unit_bound + kFwdWavesPerGroup - 1) / kFwdWavesPerGroup;
+  // Persistent grid. num_splits == 1: one wave per resident slot, but never
+  // more waves than the unit table can hold (at most (T / bq + R) row tiles
+  // x n_hu units). num_splits > 1: one work-group per CU, the partition's
+  // work-group count.
   const int32_t wg_fill = resident_workgroups();
   PA_REQUIRE(wg_fill > 0, "cannot query the compute-unit count of the current device");
-  PA_REQUIRE(unit_bound < 0x7fffffff, "the work table exceeds 2^31 - 1 units");
-  const dim3 grid(static_cast<unsigned>(wg_need < wg_fill ? wg_need : wg_fill));
+  int64_t wg = wg_fill;
+  if (a.num_splits == 1) {
+    const int64_t tile_bound =
+        a.num_q_tiles > 0 ? a.num_q_tiles
+                          : static_cast<int64_t>(a.num_tokens) / a.bq + a.num_reqs;
+    const int64_t unit_bound = tile_bound * p.n_hu;
+    PA_REQUIRE(unit_bound < 0x7fffffff, "the work table exceeds 2^31 - 1 units");
+    const int64_t wg_need = (unit_bound + kGroupUnits - 1) / kGroupUnits;
+    wg = wg_need < wg_fill ? wg_need : wg_fill;
+  }
+  const dim3 grid(static_cast<unsigned>(wg));
   const bool windowed = a.window > 0 || a.causal == 0;
   const bool paged16 = a.block_size % 16 == 0 && p.cell;
   const hipError_t err = launch_fwd_kernel(p, grid, windowed, paged16,
@@ -239,7 +263,18 @@ int32_t launch_attention(const PthAttnArgs& a, int32_t loader,
                                     hipGetErrorString(err));
   }
   if (fill_unused_splits && a.num_splits > 1) {
-    const hipError_t e2 = launch_fill_unused_splits(p, a.num_tokens, a.num_q_heads, stream);
+    CombineParams f{};
+    f.ws_lse = reinterpret_cast<const char*>(a.ws_lse);
+    f.s_wl_split = a.ws_lse_stride_split;
+    f.s_wl_tok = a.ws_lse_stride_token;
+    f.s_wl_head = a.ws_lse_stride_head;
+    f.qsl = a.query_start_loc;
+    f.num_reqs = a.num_reqs;
+    f.num_tokens = a.num_tokens;
+    f.num_q_heads = a.num_q_heads;
+    f.num_splits = a.num_splits;
+    stream_fields(a, f);
+    const hipError_t e2 = launch_fill_unused_splits(f, stream);
     if (e2 != hipSuccess)
       return fail(PTH_ATTN_ECUDA, std::string("unused-split fill launch: ") + hipGetErrorString(e2));
   }
@@ -294,12 +329,9 @@ int32_t launch_combine(const PthAttnCombineArgs& c, hipStream_t stream,
   p.num_tokens = c.num_tokens;
   p.num_q_heads = c.num_q_heads;
   p.num_splits = c.num_splits;
-  if (split_source != nullptr) {
-    p.seq_lens = split_source->seq_lens;
-    p.bq = split_source->bq;
-    p.window = split_source->window;
-    p.causal = split_source->causal;
-  }
+  if (split_source != nullptr) stream_fields(*split_source, p);
+  const int64_t rows = static_cast<int64_t>(c.num_tokens) * c.num_q_heads;
+  p.shared_rows = c.num_splits > 64 && rows < 4 * static_cast<int64_t>(resident_workgroups());
   const hipError_t err = launch_combine_kernel(p, stream);
   if (err != hipSuccess) {
     return fail(PTH_ATTN_ECUDA, std::string("combine launch: ") + hipGetErrorString(err));
@@ -396,6 +428,14 @@ int32_t pth_attn_attention_ex(const PthAttnArgs* args,
 
 int32_t pth_attn_attention(const PthAttnArgs* args, void* stream) {
   return pth_attn_attention_ex(args, nullptr, stream);
+}
+
+int32_t pth_attn_attention_kernel(const PthAttnArgs* args, void* stream) {
+  pa::clear_error();
+  const int32_t rc = check_args_abi(args);
+  if (rc != PTH_ATTN_OK) return rc;
+  return pa::launch_attention(*args, 0, static_cast<hipStream_t>(stream), nullptr, 0, 0,
+                              /*fill_unused_splits=*/false);
 }
 
 int32_t pth_attn_combine(const PthAttnCombineArgs* args, void* stream) {

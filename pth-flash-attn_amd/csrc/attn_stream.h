@@ -1,0 +1,167 @@
+// attn_stream.h -- device-side walk of the split partition (num_splits > 1),
+// shared by the attention kernel (which computes the splits), the combine
+// (which merges them) and the unused-split fill. The partition itself is
+// defined in attn_geometry.h: the 32-key chunk streams of all (request, row
+// tile, group of kGroupUnits KV-head units) laid end to end, work-group b of
+// the attention grid taking positions [b per, (b + 1) per).
+//
+// Everything here is a pure function of query_start_loc, seq_lens and the
+// launch constants, evaluated on the device, so a captured graph replays
+// correctly as the lengths grow.
+
+#pragma once
+
+#include "attn_internal.h"
+
+namespace pa {
+
+// Read-only inputs (query_start_loc, seq_lens, block_table) are read through
+// the constant address space: a wave-uniform index then becomes a scalar
+// load, which is tracked by lgkmcnt and never makes the wave wait for its
+// vector loads in flight.
+__device__ __forceinline__ int32_t ld_ro(const int32_t* base, int64_t i) {
+  return ((const int32_t __attribute__((address_space(4)))*)(base))[i];
+}
+
+// What the layout depends on.
+struct StreamDesc {
+  const int32_t* qsl;
+  const int32_t* seq_lens;
+  int32_t num_reqs;
+  int32_t bq;
+  int32_t window;
+  int32_t causal;
+  int32_t n_hg;      // groups of kGroupUnits KV-head units per row tile
+  int32_t num_wg;    // work-groups of the attention grid
+  int32_t num_splits;
+};
+
+__device__ __forceinline__ int64_t readlane64(int64_t x, int l) {
+  const uint32_t lo = __builtin_amdgcn_readlane(static_cast<uint32_t>(x), l);
+  const uint32_t hi = __builtin_amdgcn_readlane(static_cast<uint32_t>(static_cast<uint64_t>(x) >> 32), l);
+  return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
+// Inclusive prefix sum over the 64 lanes.
+__device__ __forceinline__ int64_t wave_scan64(int64_t x, int lane) {
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int64_t v = __shfl_up(x, d);
+    if (lane >= d) x += v;
+  }
+  return x;
+}
+
+__device__ __forceinline__ int32_t wave_max32(int32_t x) {
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int32_t v = __shfl_xor(x, d);
+    x = v > x ? v : x;
+  }
+  return x;
+}
+
+// Stream positions of request r (all its row tiles and groups) and the chunk
+// count of its longest row tile.
+__device__ __forceinline__ void request_positions(const StreamDesc& d, int r, int64_t& pos,
+                                                  int32_t& longest) {
+  const int q_len = d.qsl[r + 1] - d.qsl[r];
+  int32_t sum, mx;
+  request_chunks(q_len, d.seq_lens[r], d.bq, d.window, d.causal != 0, sum, mx);
+  pos = static_cast<int64_t>(sum) * d.n_hg;
+  longest = mx;
+}
+
+// Total stream positions and the positions per work-group (every lane).
+__device__ __forceinline__ int64_t stream_per(const StreamDesc& d, int lane, int64_t& total) {
+  int64_t sum = 0;
+  int32_t mx = 0;
+  for (int r0 = 0; r0 < d.num_reqs; r0 += 64) {
+    const int r = r0 + lane;
+    if (r < d.num_reqs) {
+      int64_t pos;
+      int32_t longest;
+      request_positions(d, r, pos, longest);
+      sum += pos;
+      mx = longest > mx ? longest : mx;
+    }
+  }
+  total = readlane64(wave_scan64(sum, lane), 63);
+  return chunks_per_group(total, wave_max32(mx), d.num_wg, d.num_splits);
+}
+
+// Stream positions of all requests before request r (every lane).
+__device__ __forceinline__ int64_t positions_before(const StreamDesc& d, int r, int lane) {
+  int64_t sum = 0;
+  for (int r0 = 0; r0 < r; r0 += 64) {
+    const int q = r0 + lane;
+    if (q < r) {
+      int64_t pos;
+      int32_t longest;
+      request_positions(d, q, pos, longest);
+      sum += pos;
+    }
+  }
+  return readlane64(wave_scan64(sum, lane), 63);
+}
+
+// One stream: row tile t, group hg, positions [c0, c0 + n); chunk c of it
+// covers keys [cb + 32 c, cb + 32 c + 32).
+struct StreamPos {
+  RowTile t;
+  int32_t hg;
+  int64_t c0;
+  int32_t n;
+  int32_t cb;
+};
+
+// Forward-only cursor over the requests, 64 at a time, with each lane's
+// inclusive prefix of stream positions.
+struct StreamCursor {
+  int r0 = -64;
+  int64_t base = 0;  // positions before request r0
+  int64_t end = 0;   // positions through request r0 + 63
+  int64_t incl = 0;
+};
+
+// The stream holding position P (P never decreases on a cursor). False when
+// P is past the last stream.
+__device__ __forceinline__ bool stream_locate(const StreamDesc& d, StreamCursor& c, int64_t P,
+                                              int lane, StreamPos& out) {
+  while (P >= c.end) {
+    c.r0 += 64;
+    if (c.r0 >= d.num_reqs) return false;
+    c.base = c.end;
+    const int r = c.r0 + lane;
+    int64_t pos = 0;
+    int32_t longest;
+    if (r < d.num_reqs) request_positions(d, r, pos, longest);
+    c.incl = wave_scan64(pos, lane);
+    c.end = c.base + readlane64(c.incl, 63);
+  }
+  const int64_t local = P - c.base;
+  const int j = static_cast<int>(__popcll(__ballot(c.incl <= local)));
+  const int r = c.r0 + j;
+  int64_t at = c.base + (j > 0 ? readlane64(c.incl, j - 1) : 0);
+  const int q_start = ld_ro(d.qsl, r);
+  const int q_len = ld_ro(d.qsl, r + 1) - q_start;
+  const int seq_len = ld_ro(d.seq_lens, r);
+  const int tiles = request_row_tiles(q_len, d.bq);
+  for (int k = 0; k < tiles; ++k) {
+    const RowTile t = request_tile(r, q_start, q_len, seq_len, d.bq, k);
+    const int32_t n = tile_chunks(t, d.window, d.causal != 0);
+    const int64_t span = static_cast<int64_t>(n) * d.n_hg;
+    if (P < at + span) {
+      out.t = t;
+      out.hg = static_cast<int32_t>((P - at) / n);
+      out.n = n;
+      out.c0 = at + static_cast<int64_t>(out.hg) * n;
+      out.cb = tile_chunk_base(t, d.window);
+      return true;
+    }
+    at += span;
+  }
+  return false;  // not reached: P < c.end lies in some tile of request r
+}
+
+}  // namespace pa

@@ -34,6 +34,7 @@ EXPORTED_SYMBOLS = (
     "pth_attn_attention_ex",
     "pth_attn_combine",
     "pth_attn_attention_lse",
+    "pth_attn_attention_kernel",
 )
 
 
@@ -156,6 +157,8 @@ class AttnLib:
             ctypes.POINTER(PthAttnArgs), ctypes.POINTER(PthAttnOptions), vp]
         lib.pth_attn_combine.restype = i32
         lib.pth_attn_combine.argtypes = [ctypes.POINTER(PthAttnCombineArgs), vp]
+        lib.pth_attn_attention_kernel.restype = i32
+        lib.pth_attn_attention_kernel.argtypes = [ctypes.POINTER(PthAttnArgs), vp]
         lib.pth_attn_attention_lse.restype = i32
         lib.pth_attn_attention_lse.argtypes = [
             ctypes.POINTER(PthAttnArgs), vp, ctypes.c_int64, ctypes.c_int64, vp]
@@ -170,6 +173,10 @@ class AttnLib:
 
     def attention(self, args: PthAttnArgs, stream: int | None = None) -> int:
         return self.lib.pth_attn_attention(ctypes.byref(args), stream)
+
+    def attention_kernel(self, args: PthAttnArgs, stream: int | None = None) -> int:
+        """The attention kernel alone, as the torch op launches it (see the header)."""
+        return self.lib.pth_attn_attention_kernel(ctypes.byref(args), stream)
 
     def attention_lse(self, args: PthAttnArgs, lse: Any, stream: int | None = None) -> int:
         """Run attention (+ combine) and write the natural-log LSE into `lse` [T, Hq] fp32."""

@@ -122,61 +122,78 @@ static void visible() {
   std::printf("visible ok\n");
 }
 
-// Splits: the live count is within [1, num_splits] and [count/4 rounded up];
-// the live ranges partition the tiles and differ by at most one.
-static void splits() {
-  for (int count = 0; count <= 600; ++count)
-    for (int S = 1; S <= 300; S += (S < 20 ? 1 : 7)) {
-      const int live = live_splits(count, S);
-      CHECK(live >= 1 && live <= S, "live %d", live);
-      CHECK(live == S || live == (count + kMinTilesPerSplit - 1) / kMinTilesPerSplit ||
-                (count == 0 && live == 1),
-            "live rule");
-      int prev = 0, mn = 1 << 30, mx = -1;
-      for (int s = 0; s < live; ++s) {
-        int b, e;
-        split_range(s, live, count, b, e);
-        CHECK(b == prev && e >= b, "partition");
-        prev = e;
-        mn = e - b < mn ? e - b : mn;
-        mx = e - b > mx ? e - b : mx;
-      }
-      CHECK(prev == count && mx - mn <= 1, "cover/balance");
-      if (count >= live) CHECK(mn >= 1, "no empty live split when tiles suffice");
-    }
-  // request_splits is the live count of the request's widest row tile.
-  for (int L = 1; L <= 5000; L += 37)
-    for (int q : {1, 4, 16, 33})
-      for (int W : {0, 100, 2048})
-        for (int c = 0; c < 2; ++c) {
-          if (q > L) continue;
-          const int bq = 16;
-          int want = 0;
-          for (int j = 0; j < request_row_tiles(q, bq); ++j) {
-            const RowTile t = request_tile(0, 0, q, L, bq, j);
-            const int rb = W > 0 ? range_begin(t, W) : 0;
-            const int n = kv_tile_count(rb, range_end(t, W, c));
-            const int l = live_splits(n, 256);
-            want = l > want ? l : want;
+// The chunk streams of the split partition: a row tile's chunks cover every
+// key its rows see, and no chunk is wholly outside them; the per-work-group
+// share keeps every stream within num_splits work-groups; stream_splits
+// names exactly the work-groups whose ranges meet the stream.
+static void streams() {
+  for (int L = 1; L <= 300; L += 7)
+    for (int q = 1; q <= L && q <= 40; q += 3)
+      for (int W : {0, 1, 5, 33, 64, 100})
+        for (int causal = 0; causal < 2; ++causal)
+          for (int bq : {1, 4, 16}) {
+            int32_t sum = 0, mx = 0;
+            request_chunks(q, L, bq, W, causal, sum, mx);
+            int32_t s2 = 0, m2 = 0;
+            for (int j = 0; j < request_row_tiles(q, bq); ++j) {
+              const RowTile t = request_tile(0, 0, q, L, bq, j);
+              const int cb = tile_chunk_base(t, W);
+              const int n = tile_chunks(t, W, causal);
+              CHECK(cb % kChunkTokens == 0 && n >= 1, "chunk base / count");
+              bool first_used = false, last_used = false;
+              for (int tok = t.tok_begin; tok < t.tok_begin + t.num_tok; ++tok) {
+                const int lo = key_lo(t, tok, W), hi = key_hi(t, tok, W, causal);
+                CHECK(lo >= cb && hi < cb + kChunkTokens * n, "chunks cover the keys");
+                first_used |= lo < cb + kChunkTokens;
+                last_used |= hi >= cb + kChunkTokens * (n - 1);
+              }
+              CHECK(first_used && last_used, "no chunk wholly outside the keys");
+              s2 += n;
+              m2 = n > m2 ? n : m2;
+            }
+            CHECK(sum == s2 && mx == m2, "request_chunks");
           }
-          const int got = request_splits(q, L, bq, W, c, 256);
-          // Without a window the last tile is the widest. With one, a full
-          // tile before a short last tile can reach a few more keys; the
-          // count then only changes the balance (a tile with fewer KV tiles
-          // than live splits leaves some empty, which write lse = -inf).
-          if (W == 0) CHECK(got == want, "request_splits L=%d q=%d W=%d", L, q, W);
-          CHECK(got <= want, "request_splits above the widest tile's count");
-          CHECK(got >= 1 && got <= 256, "range");
+  std::mt19937 rng(3);
+  for (int trial = 0; trial < 4000; ++trial) {
+    const int nstreams = 1 + rng() % 40;
+    std::vector<int> len(nstreams);
+    int64_t total = 0;
+    int32_t mx = 0;
+    for (int& n : len) {
+      n = 1 + rng() % (trial % 3 == 0 ? 5000 : 200);
+      total += n;
+      mx = n > mx ? n : mx;
+    }
+    const int num_wg = 1 + rng() % 300;
+    const int S = 2 + rng() % 300;
+    const int64_t per = chunks_per_group(total, mx, num_wg, S);
+    CHECK(per >= kMinChunksPerSplit && per * num_wg >= total, "per covers the total");
+    int64_t c0 = 0;
+    for (int n : len) {
+      int first, live;
+      stream_splits(c0, n, per, first, live);
+      CHECK(live >= 1 && live <= S, "live %d > S %d (n=%d per=%lld)", live, S, n, (long long)per);
+      // Brute force: the work-groups whose range meets [c0, c0 + n).
+      int bf_first = -1, bf_count = 0;
+      for (int b = 0; b < num_wg; ++b) {
+        const int64_t lo = b * per, hi = lo + per;
+        if (lo < c0 + n && hi > c0) {
+          if (bf_first < 0) bf_first = b;
+          ++bf_count;
         }
-  CHECK(request_splits(0, 10, 4, 0, true, 8) == 0, "empty request");
-  std::printf("splits ok\n");
+      }
+      CHECK(bf_first == first && bf_count == live, "stream_splits");
+      c0 += n;
+    }
+  }
+  std::printf("streams ok\n");
 }
 
 int main() {
   div32();
   row_tiles();
   visible();
-  splits();
+  streams();
   std::printf("ALL OK\n");
   return fails;
 }
