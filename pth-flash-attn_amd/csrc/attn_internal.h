@@ -64,6 +64,9 @@ struct AttnParams {
   // (and lse_out) by the attention kernel itself, and the combine skips it.
   // Off when the caller combines all num_splits splits itself.
   int32_t direct_single;
+  // Row-block kernel (attn_rows.hip): query tokens per block and KV heads.
+  int32_t blk_tok;
+  int32_t num_kv_heads;
   float scale_log2;  // softmax_scale * log2(e)
 };
 
@@ -120,6 +123,11 @@ int32_t launch_combine(const PthAttnCombineArgs& c, hipStream_t stream,
 int32_t resident_workgroups();
 hipError_t launch_fwd_kernel(const AttnParams& p, dim3 grid, bool windowed,
                              bool paged16, bool q_f16, hipStream_t stream);
+// The row-block kernel (num_splits == 1, paged cell caches) and the query
+// tokens of one of its blocks for GQA group `group`.
+hipError_t launch_rows_kernel(const AttnParams& p, dim3 grid, bool windowed, bool q_f16,
+                              hipStream_t stream);
+int32_t rows_block_tokens(int32_t group);
 hipError_t launch_combine_kernel(const CombineParams& c, hipStream_t stream);
 hipError_t launch_fill_unused_splits(const CombineParams& c, hipStream_t stream);
 

@@ -234,6 +234,8 @@ int32_t launch_attention(const PthAttnArgs& a, int32_t loader,
   p.causal = a.causal;
   p.out_dtype = a.out_dtype;
   p.direct_single = fill_unused_splits ? 0 : 1;
+  p.blk_tok = rows_block_tokens(group);
+  p.num_kv_heads = a.num_kv_heads;
   p.scale_log2 = a.softmax_scale * kLog2e;
 
   // Persistent grid. num_splits == 1: one wave per resident slot, but never
@@ -252,11 +254,23 @@ int32_t launch_attention(const PthAttnArgs& a, int32_t loader,
     const int64_t wg_need = (unit_bound + kGroupUnits - 1) / kGroupUnits;
     wg = wg_need < wg_fill ? wg_need : wg_fill;
   }
-  const dim3 grid(static_cast<unsigned>(wg));
   const bool windowed = a.window > 0 || a.causal == 0;
   const bool paged16 = a.block_size % 16 == 0 && p.cell;
-  const hipError_t err = launch_fwd_kernel(p, grid, windowed, paged16,
-                                           a.q_dtype == PTH_ATTN_F16, stream);
+  // Row tiles of 64 rows (the planner's prefill and wide-verify plans) on a
+  // single split: the row-block kernel, whose 8 waves share each key chunk
+  // (one work-group per CU, never more than there are blocks).
+  const bool row_blocks = a.num_splits == 1 && paged16 && rows >= 64;
+  hipError_t err;
+  if (row_blocks) {
+    const int64_t blocks =
+        (static_cast<int64_t>(a.num_tokens) / p.blk_tok + a.num_reqs) * a.num_kv_heads;
+    PA_REQUIRE(blocks < 0x7fffffff, "the block table exceeds 2^31 - 1 blocks");
+    const dim3 grid(static_cast<unsigned>(blocks < wg_fill ? blocks : wg_fill));
+    err = launch_rows_kernel(p, grid, windowed, a.q_dtype == PTH_ATTN_F16, stream);
+  } else {
+    const dim3 grid(static_cast<unsigned>(wg));
+    err = launch_fwd_kernel(p, grid, windowed, paged16, a.q_dtype == PTH_ATTN_F16, stream);
+  }
   if (err != hipSuccess) {
     return fail(PTH_ATTN_ECUDA, std::string("attention launch (D=128, rows=") +
                                     std::to_string(rows) + "): " +

@@ -1,0 +1,710 @@
+// attn_rows.hip -- the gfx950 row-block kernel: num_splits == 1 launches
+// whose row tiles hold many query rows (chunked prefill, long verify
+// windows, mixed prefill + decode batches), D = 128, paged cell caches.
+//
+// Why a second kernel. The unit kernels of attn_fwd.hip give every 16-row
+// group its own wave and its own pass over the keys: right for decode, where
+// the rows of a KV head are few and the bytes are read once, but a 2048-token
+// prefill chunk has 8192 rows per KV head, and 512 passes over the same keys
+// make the launch L2-bandwidth bound (and spend the int8 -> bf16 conversion
+// 512 times per key). Here a work-group of 8 waves takes a *row block*: up to
+// 256 rows (256 / G query tokens) of one request and one KV head, and the 8
+// waves share one stream of 32-key chunks staged in LDS by direct-to-LDS
+// loads, each wave computing its 32 rows (two 16-row MFMA groups that share
+// the converted K and V operands) against every chunk.
+//
+// A row block with fewer rows (a decode token: G rows) has fewer row sets
+// of 32 rows than waves; its waves then split the keys instead: RS row sets
+// (RS a power of two) times KP = 8 / RS key parts, the parts' partial
+// (O, m, l) merged through LDS at the end in a fixed order. So a long decode
+// row in a mixed batch runs on 8 waves, not one, and no wave idles.
+//
+// Pipeline. Each part has a ring of 16 / KP chunk slots in LDS. At step k
+// every wave waits for its own share of the loads of chunk k (the 9 loads of
+// a chunk are spread over the RS waves of the part), then the work-group
+// meets at a barrier, after which chunk k is complete in LDS and every wave
+// has finished reading chunk k - 1, so chunk k + A (A chunks ahead) is
+// issued into the slot that chunk k - 1 left, and chunk k is computed. The
+// numerics are those of attn_fwd.hip's chunk step (reference
+// attn_kernel.cuh:540-600, softmax.cuh:91-170).
+//
+// Work order. Blocks are (request, token block, KV head), KV head fastest,
+// the token blocks of a request from its last (longest key range) to its
+// first; work-group b of W takes block b of each round of W blocks, in
+// reversed order on odd rounds, so long and short blocks pair up.
+
+#include "attn_device.h"
+
+namespace pa {
+namespace {
+
+constexpr int kRowWaves = kFwdWaves;              // waves per work-group
+constexpr int kWaveRows = 2 * kRowsPerWave;       // rows per wave
+constexpr int kBlockRows = kRowWaves * kWaveRows;  // rows per block
+constexpr int kRowSlots = 16;                     // LDS chunk slots per work-group
+constexpr int kRowAhead = 3;                      // chunks in flight per part, at most
+// Partial state of one wave for the merge of key parts: O (2 groups x 8
+// f32x4 per lane), then m and l (2 groups x 1 float per lane each).
+constexpr int kMergeO = 2 * 8 * 16 * 64;
+constexpr int kMergeBytes = kMergeO + 2 * 2 * 4 * 64;
+static_assert((kRowWaves - 1) * kMergeBytes <= kRowSlots * kSlotBytes,
+              "the merge area must fit the chunk slots");
+
+__device__ __forceinline__ void wg_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+// One row block, uniform across the work-group.
+struct Block {
+  RowTile t;
+  int kvh;
+  int rows;          // num_tok * G
+  int log_rs;        // row sets of kWaveRows rows: RS = 1 << log_rs
+  int kp;            // key parts: kRowWaves / RS
+  int c_begin;       // first chunk's key (32-aligned)
+  int n_chunks;      // chunks covering the keys of any row of the block
+  int ld_lo, ld_hi;  // keys the block reads
+};
+
+template <bool kWindow>
+__device__ __forceinline__ void make_block(const AttnParams& p, const RowTile& t, int kvh,
+                                           Block& B) {
+  const int window = kWindow ? p.window : 0;
+  const bool causal = kWindow ? (p.causal != 0) : true;
+  B.t = t;
+  B.kvh = kvh;
+  B.rows = t.num_tok * p.group;
+  const int sets = (B.rows + kWaveRows - 1) / kWaveRows;
+  int lr = 0;
+  while ((1 << lr) < sets) ++lr;
+  B.log_rs = lr;
+  B.kp = kRowWaves >> lr;
+  B.ld_lo = range_begin(t, window);
+  B.ld_hi = range_end(t, window, causal);
+  B.c_begin = B.ld_lo & ~(kChunkTokens - 1);
+  B.n_chunks = B.c_begin < B.ld_hi ? (B.ld_hi - B.c_begin + kChunkTokens - 1) / kChunkTokens : 0;
+}
+
+// The blocks of one work-group, in order (a prefix sum over requests, 64 per
+// wave instruction, as the unit table of attn_fwd.hip).
+template <bool kWindow>
+struct BlockWalk {
+  int r0 = -64;
+  int u0 = 0, u1 = 0;
+  int incl = 0;
+  int round = 0;
+
+  __device__ __forceinline__ bool next(const AttnParams& p, int lane, Block& B) {
+    const int W = gridDim.x;
+    const int b = blockIdx.x;
+    const int u = round * W + ((round & 1) ? W - 1 - b : b);
+    ++round;
+    while (u >= u1) {
+      r0 += 64;
+      u0 = u1;
+      if (r0 >= p.num_reqs) return false;
+      const int r = r0 + lane;
+      const int units = r < p.num_reqs
+                            ? request_row_tiles(p.qsl[r + 1] - p.qsl[r], p.blk_tok) * p.num_kv_heads
+                            : 0;
+      int x = units;
+#pragma unroll
+      for (int dd = 1; dd < 64; dd <<= 1) {
+        const int v = __shfl_up(x, dd);
+        if (lane >= dd) x += v;
+      }
+      incl = x;
+      u1 = u0 + __builtin_amdgcn_readlane(x, 63);
+    }
+    const int local = u - u0;
+    const int j = static_cast<int>(__popcll(__ballot(incl <= local)));
+    const int req = r0 + j;
+    const int u_loc = local - (j > 0 ? __builtin_amdgcn_readlane(incl, j - 1) : 0);
+    const int q_start = ld_ro(p.qsl, req);
+    const int q_len = ld_ro(p.qsl, req + 1) - q_start;
+    const int seq_len = ld_ro(p.seq_lens, req);
+    const int nb = request_row_tiles(q_len, p.blk_tok);
+    const int jb = u_loc / p.num_kv_heads;
+    const int kvh = u_loc - jb * p.num_kv_heads;
+    const RowTile t = request_tile(req, q_start, q_len, seq_len, p.blk_tok, nb - 1 - jb);
+    make_block<kWindow>(p, t, kvh, B);
+    return true;
+  }
+};
+
+// The 32 rows [row0, row0 + 32) of a block as one wave sees them.
+struct RowSet {
+  bool has_rows;
+  bool two;                // rows row0 + 16 .. exist
+  int w_lo_min, w_lo_max;  // key_lo over the rows
+  int w_hi_min, w_hi_max;  // key_hi over the rows
+};
+
+template <bool kWindow>
+__device__ __forceinline__ RowSet make_rowset(const AttnParams& p, const Block& B, int row0) {
+  const int window = kWindow ? p.window : 0;
+  const bool causal = kWindow ? (p.causal != 0) : true;
+  RowSet R;
+  const int n = B.rows - row0;
+  R.has_rows = n > 0;
+  R.two = n > kRowsPerWave;
+  R.w_lo_min = R.w_lo_max = 0;
+  R.w_hi_min = R.w_hi_max = -1;
+  if (!R.has_rows) return R;
+  const int last = row0 + (n < kWaveRows ? n : kWaveRows) - 1;
+  const int tok_first = B.t.tok_begin + static_cast<int>(p.g_div.div(row0));
+  const int tok_last = B.t.tok_begin + static_cast<int>(p.g_div.div(last));
+  R.w_lo_min = key_lo(B.t, tok_first, window);
+  R.w_lo_max = key_lo(B.t, tok_last, window);
+  R.w_hi_min = key_hi(B.t, tok_first, window, causal);
+  R.w_hi_max = key_hi(B.t, tok_last, window, causal);
+  return R;
+}
+
+// A 16-row group of the block as a Unit (for unit_lanes and finish).
+__device__ __forceinline__ Unit group_unit(const Block& B, int row0) {
+  Unit U;
+  U.t = B.t;
+  U.s = 0;
+  U.live = 1;
+  U.kvh = B.kvh;
+  U.rg = 0;
+  U.rows = B.rows;
+  U.row0 = row0;
+  U.has_rows = row0 < B.rows;
+  return U;
+}
+
+// Loads of the block's chunks: per-lane offsets of the KV head's cells (as
+// the paged producer of attn_fwd.hip), and the pages of the next chunk to
+// issue, looked up one chunk ahead so that an issue never waits for the
+// block table.
+struct RowLoader {
+  uint32_t off_k[2], off_v[2], off_s;
+  int64_t bt0;
+  int32_t page[2], slot0[2];
+};
+
+__device__ __forceinline__ void row_loader(const AttnParams& p, const Block& B, int lane,
+                                           RowLoader& Ld) {
+  const uint32_t kq = lane >> 3, piece = lane & 7;
+  const uint32_t head = static_cast<uint32_t>(B.kvh) * p.cell_head;
+  const uint32_t sw = 16u * (piece ^ kq);
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const uint32_t row = (8u * h + kq) * p.cell_slot + head + sw;
+    Ld.off_k[h] = row + p.cell_off[0];
+    Ld.off_v[h] = row + p.cell_off[1];
+  }
+  Ld.off_s = static_cast<uint32_t>(lane & 15) * p.cell_slot + head +
+             (lane < 32 ? p.cell_off[2] : p.cell_off[3]);
+  Ld.bt0 = static_cast<int64_t>(B.t.req) * p.bt_stride;
+}
+
+// Pages of the chunk at key c (scalar loads). A 16-key group outside the
+// block's keys reads page 0 (masked later).
+__device__ __forceinline__ void rows_pages(const AttnParams& p, const Block& B, int c,
+                                           RowLoader& Ld) {
+#pragma unroll
+  for (int sub = 0; sub < 2; ++sub) {
+    const int c16 = c + 16 * sub;
+    Ld.page[sub] = 0;
+    Ld.slot0[sub] = 0;
+    if (c16 < B.ld_hi && c16 + 16 > B.ld_lo) {
+      const int blk = static_cast<int>(p.bs_div.div(c16));
+      Ld.slot0[sub] = c16 - blk * static_cast<int>(p.bs_div.d);
+      Ld.page[sub] = ld_ro(p.block_table, Ld.bt0 + blk);
+    }
+  }
+}
+
+// This wave's share of the 9 loads of the chunk whose pages Ld holds: loads
+// d with d % RS == rs (d < 4: K rows 8d .. 8d + 7; d < 8: V rows
+// 8(d - 4) ..; d = 8: the 64 scales), laid out as the paged producer of
+// attn_fwd.hip lays them out.
+__device__ __forceinline__ void issue_rows_chunk(const AttnParams& p, const RowLoader& Ld,
+                                                 char* slot, int rs, int mask, int lane) {
+  const char* base[2];
+#pragma unroll
+  for (int sub = 0; sub < 2; ++sub)
+    base[sub] = p.cell_base +
+                static_cast<uint64_t>(static_cast<uint32_t>(Ld.page[sub])) * p.cell_block +
+                static_cast<uint32_t>(Ld.slot0[sub]) * p.cell_slot;
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    if ((d & mask) == rs) dma16(base[d >> 1] + Ld.off_k[d & 1], slot + kSlotK + 1024 * d);
+    if (((d + 4) & mask) == rs) dma16(base[d >> 1] + Ld.off_v[d & 1], slot + kSlotV + 1024 * d);
+  }
+  if ((8 & mask) == rs) dma4(((lane >> 4) & 1 ? base[1] : base[0]) + Ld.off_s, slot + kSlotScale);
+}
+
+// Loads per chunk issued by row set rs of RS = mask + 1.
+__device__ __forceinline__ int rows_chunk_loads(int mask, int rs) {
+  int n = 0;
+#pragma unroll
+  for (int d = 0; d < kDmaPerChunk; ++d) n += (d & mask) == rs ? 1 : 0;
+  return n;
+}
+
+// One 32-key chunk at key c for the wave's two 16-row groups: compute_chunk
+// of attn_device.h, each K and V operand used by both groups. `ops` gives
+// the bf16 operands (converted from the int8 chunk, or read from the
+// work-group's converted copy): ops.sc() the lane's scale, ops.k(sub, j),
+// ops.load_v() (issued before the softmax) and ops.v(j).
+template <bool kF16Q, class Ops>
+__device__ __forceinline__ void compute_rows(const RowSet& R, const Lanes (&L)[2], int c, Ops& ops,
+                                             const bf16x8 (&qb)[2][4], const bf16x8 (&qlo)[2][4],
+                                             float scl, State (&st)[2]) {
+  const float sc1 = ops.sc() * scl;
+  const float ks[8] = {row_bcast<0>(sc1), row_bcast<1>(sc1), row_bcast<2>(sc1),
+                       row_bcast<3>(sc1), row_bcast<4>(sc1), row_bcast<5>(sc1),
+                       row_bcast<6>(sc1), row_bcast<7>(sc1)};
+  float vs[8] = {row_bcast<8>(sc1),  row_bcast<9>(sc1),  row_bcast<10>(sc1),
+                 row_bcast<11>(sc1), row_bcast<12>(sc1), row_bcast<13>(sc1),
+                 row_bcast<14>(sc1), row_bcast<15>(sc1)};
+  const int ng = R.two ? 2 : 1;
+  bool fresh[2];
+  float m_use[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    fresh[i] = st[i].m == kNegInf;
+    m_use[i] = fresh[i] ? 0.0f : st[i].m;
+  }
+  float t[2][8];
+#pragma unroll
+  for (int sub = 0; sub < 2; ++sub) {
+    f32x4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const bf16x8 a = ops.k(sub, j);
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        if (i < ng) {
+          acc[i] = mfma(a, qb[i][j], acc[i]);
+          if constexpr (kF16Q) acc[i] = mfma(a, qlo[i][j], acc[i]);
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) t[i][4 * sub + e] = fmaf(acc[i][e], ks[4 * sub + e], -m_use[i]);
+  }
+  ops.load_v();
+  if (c < R.w_lo_max || c + kChunkTokens - 1 > R.w_hi_min) {
+    // Keys outside a row's range get p = 0; keys outside every row's range
+    // (possibly outside the request: any bits, a scale included) also a zero
+    // V scale. Keys inside some row's range are cache data of the request.
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int key = c + 16 * (e >> 2) + 4 * L[0].g + (e & 3);
+      if (key < R.w_lo_min || key > R.w_hi_max) vs[e] = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+        if (key < L[i].lo || key > L[i].hi) t[i][e] = kNegInf;
+    }
+  }
+  bf16x8 p_hi[2], p_lo[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    if (i >= ng) continue;
+    float mx = t[i][0];
+#pragma unroll
+    for (int e = 1; e < 8; ++e) mx = fmaxf(mx, t[i][e]);
+    mx = xor_max(mx);
+    const bool grow = fresh[i] ? mx > kNegInf : mx > kRescaleSlack;
+    if (__ballot(grow) != 0) {
+      const float alpha = grow && !fresh[i] ? __builtin_amdgcn_exp2f(-mx) : 1.0f;
+      st[i].l *= alpha;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) st[i].o[j] *= alpha;
+      const float shift = grow ? mx : 0.0f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) t[i][e] -= shift;
+      st[i].m = grow ? m_use[i] + mx : st[i].m;
+    }
+    float pv[8];
+    float lsum = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float pe = __builtin_amdgcn_exp2f(t[i][e]);
+      lsum += pe;
+      pv[e] = pe * vs[e];
+    }
+    st[i].l += lsum;
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) {
+      const bf16x2 h = pack_bf16(pv[e], pv[e + 1]);
+      const uint32_t hb = __builtin_bit_cast(uint32_t, h);
+      const float h0 = __builtin_bit_cast(float, hb << 16);
+      const float h1 = __builtin_bit_cast(float, hb & 0xffff0000u);
+      const bf16x2 lw = pack_bf16(pv[e] - h0, pv[e + 1] - h1);
+      p_hi[i][e] = h[0];
+      p_hi[i][e + 1] = h[1];
+      p_lo[i][e] = lw[0];
+      p_lo[i][e + 1] = lw[1];
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const bf16x8 vcol = ops.v(j);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      if (i < ng) {
+        st[i].o[j] = mfma(vcol, p_hi[i], st[i].o[j]);
+        st[i].o[j] = mfma(vcol, p_lo[i], st[i].o[j]);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Wide blocks (one key part: all 8 waves compute every chunk). The int8 ->
+// bf16 conversion is shared: each wave converts one eighth of a chunk into a
+// bf16 copy in LDS, one chunk ahead of the compute, and every wave reads its
+// MFMA operands from the copy. Copy layout (16 KB, lane-contiguous):
+//   K: [sub 2][j 4][lane 64] x 16 B  -- bf16 K[16 sub + (l % 16)][32 (l / 16) + 8 j ..]
+//   V: [j 8][lane 64] x 16 B         -- bf16 V[tv(e)][8 (l % 16) + j], e = 0..7
+// Wave w converts K operand (sub, j) = (w / 4, w % 4) and V column j = w.
+constexpr int kWideSlots = 8;  // int8 chunk slots of a wide block
+constexpr int kWideAhead = 3;  // int8 chunks in flight beyond the one being converted
+constexpr int kCopyBytes = 16384;
+constexpr int kCopyBase = kWideSlots * kSlotBytes;
+static_assert(kCopyBase + 2 * kCopyBytes <= kRowSlots * kSlotBytes, "wide-block LDS");
+static_assert(kWideAhead + 2 <= kWideSlots, "a refilled slot must be two chunks old");
+
+__device__ __forceinline__ uint32_t ds_read_i8(uint32_t a) {
+  uint32_t v;
+  asm volatile("ds_read_i8 %0, %1" : "=v"(v) : "v"(a));
+  return v;
+}
+template <int kOff>
+__device__ __forceinline__ void ds_write16(uint32_t a, u32x4 v) {
+  asm volatile("ds_write_b128 %0, %1 offset:%2" ::"v"(a), "v"(v), "n"(kOff) : "memory");
+}
+
+// Per-lane LDS offsets of the conversion reads (chunk slot relative).
+struct ConvOffsets {
+  uint32_t k;     // 8 bytes of K
+  uint32_t v[4];  // byte j of the V run of key 4g + q (+ 2048: key 16 + 4g + q)
+};
+
+__device__ __forceinline__ ConvOffsets conv_offsets(int wave, int lane) {
+  const int r16 = lane & 15, g = lane >> 4;
+  const int sub = wave >> 2, j = wave & 3;
+  ConvOffsets o;
+  o.k = kSlotK + swz(16 * sub + r16, 2 * g + (j >> 1)) + 8 * (j & 1);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) o.v[q] = kSlotV + swz(4 * g + q, r16 >> 1) + 8 * (r16 & 1) + wave;
+  return o;
+}
+
+// Wave `wave`'s eighth of the chunk in int8 slot `slot` -> bf16 copy `copy`.
+__device__ __forceinline__ void convert_share(uint32_t slot, uint32_t copy, const ConvOffsets& o,
+                                              int wave, int lane) {
+  u32x2 kw = ds_read8<0>(slot + o.k);
+  uint32_t vb[8];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    vb[q] = ds_read_i8(slot + o.v[q]);
+    vb[4 + q] = ds_read_i8(slot + o.v[q] + 2048);
+  }
+  asm volatile("s_waitcnt lgkmcnt(0)"
+               : "+v"(kw), "+v"(vb[0]), "+v"(vb[1]), "+v"(vb[2]), "+v"(vb[3]), "+v"(vb[4]),
+                 "+v"(vb[5]), "+v"(vb[6]), "+v"(vb[7])
+               :
+               : "memory");
+  const bf16x8 ka = i8x8_to_bf16(kw[0], kw[1]);
+  // V column: the 8 keys in e order (tv(e) = 16 (e / 4) + 4 g + e % 4).
+  bf16x2 pr[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    pr[e] = pack_bf16(static_cast<float>(static_cast<int32_t>(vb[2 * e])),
+                      static_cast<float>(static_cast<int32_t>(vb[2 * e + 1])));
+  const bf16x8 va = {pr[0][0], pr[0][1], pr[1][0], pr[1][1], pr[2][0], pr[2][1], pr[3][0], pr[3][1]};
+  const uint32_t dst = copy + wave * 1024 + lane * 16;
+  ds_write16<0>(dst, __builtin_bit_cast(u32x4, ka));
+  ds_write16<8192>(dst, __builtin_bit_cast(u32x4, va));
+}
+
+// Operands of compute_rows from the int8 chunk in registers.
+struct Int8Ops {
+  const Chunk& ch;
+  __device__ __forceinline__ float sc() const { return ch.sc; }
+  __device__ __forceinline__ bf16x8 k(int sub, int j) const {
+    const u32x4& w = ch.k[sub][j >> 1];
+    return (j & 1) ? i8x8_to_bf16(w[2], w[3]) : i8x8_to_bf16(w[0], w[1]);
+  }
+  __device__ __forceinline__ void load_v() const {}
+  __device__ __forceinline__ bf16x8 v(int j) const { return column_to_bf16(ch.v, j); }
+};
+
+// Operands of compute_rows from a bf16 copy: K and the scale read at
+// construction, V read by load_v.
+struct CopyOps {
+  uint32_t a;  // copy + 16 lane
+  u32x4 kk[8];
+  u32x4 vv[8];
+  float s;
+
+  __device__ __forceinline__ CopyOps(uint32_t copy, uint32_t scale_addr, int lane)
+      : a(copy + lane * 16) {
+    kk[0] = ds_read16<0>(a);
+    kk[1] = ds_read16<1024>(a);
+    kk[2] = ds_read16<2048>(a);
+    kk[3] = ds_read16<3072>(a);
+    kk[4] = ds_read16<4096>(a);
+    kk[5] = ds_read16<5120>(a);
+    kk[6] = ds_read16<6144>(a);
+    kk[7] = ds_read16<7168>(a);
+    s = ds_read4(scale_addr);
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(kk[0]), "+v"(kk[1]), "+v"(kk[2]), "+v"(kk[3]), "+v"(kk[4]), "+v"(kk[5]),
+                   "+v"(kk[6]), "+v"(kk[7]), "+v"(s)
+                 :
+                 : "memory");
+  }
+  __device__ __forceinline__ float sc() const { return s; }
+  __device__ __forceinline__ bf16x8 k(int sub, int j) const {
+    return __builtin_bit_cast(bf16x8, kk[4 * sub + j]);
+  }
+  __device__ __forceinline__ void load_v() {
+    vv[0] = ds_read16<8192>(a);
+    vv[1] = ds_read16<9216>(a);
+    vv[2] = ds_read16<10240>(a);
+    vv[3] = ds_read16<11264>(a);
+    vv[4] = ds_read16<12288>(a);
+    vv[5] = ds_read16<13312>(a);
+    vv[6] = ds_read16<14336>(a);
+    vv[7] = ds_read16<15360>(a);
+  }
+  // The first use waits for all eight (the softmax in between hides the
+  // LDS latency).
+  __device__ __forceinline__ bf16x8 v(int j) {
+    if (j == 0)
+      asm volatile("s_waitcnt lgkmcnt(0)"
+                   : "+v"(vv[0]), "+v"(vv[1]), "+v"(vv[2]), "+v"(vv[3]), "+v"(vv[4]),
+                     "+v"(vv[5]), "+v"(vv[6]), "+v"(vv[7])
+                   :
+                   : "memory");
+    return __builtin_bit_cast(bf16x8, vv[j]);
+  }
+};
+
+// Merge area of writer w (a wave of key part >= 1): O, m, l per lane.
+__device__ __forceinline__ char* merge_area(char* lds, int w) { return lds + w * kMergeBytes; }
+
+// (Loops over the two groups are unrolled with constant indices: a
+// run-time index would move the states to scratch memory.)
+__device__ __forceinline__ void merge_store(char* a, int lane, const State (&st)[2], int ng) {
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    if (i >= ng) break;
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      *reinterpret_cast<f32x4*>(a + ((i * 8 + j) * 64 + lane) * 16) = st[i].o[j];
+    *reinterpret_cast<float*>(a + kMergeO + (i * 64 + lane) * 4) = st[i].m;
+    *reinterpret_cast<float*>(a + kMergeO + 512 + (i * 64 + lane) * 4) = st[i].l;
+  }
+}
+
+// st := st (+) the partial of area a: the same rows, another part of the keys.
+__device__ __forceinline__ void merge_add(const char* a, int lane, State& st, int i) {
+  const float mj = *reinterpret_cast<const float*>(a + kMergeO + (i * 64 + lane) * 4);
+  const float lj = *reinterpret_cast<const float*>(a + kMergeO + 512 + (i * 64 + lane) * 4);
+  const float M = fmaxf(st.m, mj);
+  if (M == kNegInf) return;  // neither part has seen a key of this row
+  const float a0 = __builtin_amdgcn_exp2f(st.m - M);
+  const float a1 = __builtin_amdgcn_exp2f(mj - M);
+  st.l = st.l * a0 + lj * a1;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const f32x4 oj = *reinterpret_cast<const f32x4*>(a + ((i * 8 + j) * 64 + lane) * 16);
+    st.o[j] = st.o[j] * a0 + oj * a1;
+  }
+  st.m = M;
+}
+
+// The chunk loop of a wide block. Step k: wait for this wave's loads of
+// chunk k + 1, barrier (chunk k + 1 is in LDS, the bf16 copy of chunk k is
+// complete, every wave is done with the copy of chunk k - 1), refill the
+// int8 slot of chunk k - 4, convert this wave's share of chunk k + 1 into
+// the copy chunk k - 1 used, compute chunk k from its copy.
+template <bool kF16Q>
+__device__ __forceinline__ void wide_block(const AttnParams& p, const Block& B, const RowSet& R,
+                                           const Lanes (&L)[2], RowLoader& Ld,
+                                           const bf16x8 (&qb)[2][4], const bf16x8 (&qlo)[2][4],
+                                           float scl, State (&st)[2], char* lds, uint32_t lds_base,
+                                           const ReadOffsets& ro, const ConvOffsets& cvo,
+                                           int wave, int lane) {
+  const int len = B.n_chunks;
+  if (len == 0) return;
+  constexpr int mask = kRowWaves - 1;
+  const int nload = rows_chunk_loads(mask, wave);
+  const uint32_t copy0 = lds_base + kCopyBase;
+  rows_pages(p, B, B.c_begin, Ld);
+  for (int i = 0; i <= kWideAhead && i < len; ++i) {
+    issue_rows_chunk(p, Ld, lds + i * kSlotBytes, wave, mask, lane);
+    if (i + 1 < len) rows_pages(p, B, B.c_begin + kChunkTokens * (i + 1), Ld);
+  }
+  {
+    const int last = kWideAhead < len - 1 ? kWideAhead : len - 1;
+    wait_vmcnt_dyn(nload * last);
+  }
+  wg_barrier();
+  convert_share(lds_base, copy0, cvo, wave, lane);
+  for (int k = 0; k < len; ++k) {
+    if (k + 1 < len) {
+      const int last = k + kWideAhead < len - 1 ? k + kWideAhead : len - 1;
+      wait_vmcnt_dyn(nload * (last - k - 1));
+    }
+    wait_lgkmcnt0();  // this wave's copy writes
+    wg_barrier();
+    if (k + 1 + kWideAhead < len)
+      issue_rows_chunk(p, Ld, lds + ((k + 1 + kWideAhead) % kWideSlots) * kSlotBytes, wave, mask,
+                       lane);
+    if (k + 1 < len)
+      convert_share(lds_base + ((k + 1) % kWideSlots) * kSlotBytes,
+                    copy0 + ((k + 1) & 1) * kCopyBytes, cvo, wave, lane);
+    const int c = B.c_begin + kChunkTokens * k;
+    if (R.has_rows && c <= R.w_hi_max && c + kChunkTokens > R.w_lo_min) {
+      CopyOps ops(copy0 + (k & 1) * kCopyBytes, lds_base + (k % kWideSlots) * kSlotBytes + ro.s,
+                  lane);
+      compute_rows<kF16Q>(R, L, c, ops, qb, qlo, scl, st);
+    }
+    if (k + 2 + kWideAhead < len)
+      rows_pages(p, B, B.c_begin + kChunkTokens * (k + 2 + kWideAhead), Ld);
+  }
+}
+
+template <bool kWindow, bool kF16Q>
+__global__ __launch_bounds__(kRowWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void attn_fwd_rows(const AttnParams p) {
+  __shared__ __attribute__((aligned(16))) char lds[kRowSlots * kSlotBytes];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t lds_base = lds_offset(lds);
+  const ReadOffsets ro = read_offsets(lane);
+  const float scl = scale_factor(lane & 15, p.scale_log2);
+  const ConvOffsets cvo = conv_offsets(wave, lane);
+  BlockWalk<kWindow> walk;
+  Block B;
+  while (walk.next(p, lane, B)) {
+    // The previous block's merge reads of the slots are done.
+    __syncthreads();
+    const int mask = (1 << B.log_rs) - 1;
+    const int rs = wave & mask;
+    const int part = wave >> B.log_rs;
+    const int kp = B.kp;
+    const int ns = kRowSlots / kp;
+    // A part of one wave (RS == 1) owns its slots: it refills the slot it
+    // has just read and needs no barrier, so its waves stream independently.
+    // Parts of several waves refill a slot only after the barrier that
+    // follows every wave's read of it.
+    const bool solo = mask == 0;
+    const int room = solo ? ns : ns - 1;
+    const int ahead = kRowAhead < room ? kRowAhead : room;
+    const int pc0 = part * B.n_chunks / kp;
+    const int len = (part + 1) * B.n_chunks / kp - pc0;
+    const int steps = (B.n_chunks + kp - 1) / kp;
+    char* ring = lds + part * ns * kSlotBytes;
+    const uint32_t ring_base = lds_base + part * ns * kSlotBytes;
+    const int nload = rows_chunk_loads(mask, rs);
+
+    const int row0 = rs * kWaveRows;
+    const RowSet R = make_rowset<kWindow>(p, B, row0);
+    const Unit U0 = group_unit(B, row0), U1 = group_unit(B, row0 + kRowsPerWave);
+    Lanes L[2];
+    L[0] = unit_lanes<kWindow>(p, U0, lane);
+    L[1] = R.two ? unit_lanes<kWindow>(p, U1, lane) : L[0];
+    bf16x8 qb[2][4], qlo[2][4];
+    if (R.has_rows) {
+      load_q<kF16Q>(p, L[0], qb[0], qlo[0]);
+      if (R.two) load_q<kF16Q>(p, L[1], qb[1], qlo[1]);
+    }
+    // Q has landed (a compiler-visible vmcnt(0): the chunk waits below are
+    // asm the compiler does not see).
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+    State st[2];
+    state_reset(st[0]);
+    state_reset(st[1]);
+
+    RowLoader Ld;
+    row_loader(p, B, lane, Ld);
+    if (kp == 1) {
+      wide_block<kF16Q>(p, B, R, L, Ld, qb, qlo, scl, st, lds, lds_base, ro, cvo, wave, lane);
+      if (R.has_rows) {
+        epilogue(p, U0, L[0], st[0]);
+        if (R.two) epilogue(p, U1, L[1], st[1]);
+      }
+      continue;
+    }
+    const int c0 = B.c_begin + kChunkTokens * pc0;
+    if (len > 0) rows_pages(p, B, c0, Ld);
+    for (int i = 0; i < ahead && i < len; ++i) {
+      issue_rows_chunk(p, Ld, ring + i * kSlotBytes, rs, mask, lane);
+      if (i + 1 < len) rows_pages(p, B, c0 + kChunkTokens * (i + 1), Ld);
+    }
+    const int nsteps = solo ? len : steps;
+    for (int k = 0; k < nsteps; ++k) {
+      if (k < len) {
+        const int last = k + ahead - 1 < len - 1 ? k + ahead - 1 : len - 1;
+        wait_vmcnt_dyn(nload * (last - k));
+      }
+      // After the barrier chunk k is complete in LDS and every wave is done
+      // reading chunk k - 1.
+      if (!solo) wg_barrier();
+      const int c = c0 + kChunkTokens * k;
+      const bool mine = k < len && R.has_rows && c <= R.w_hi_max && c + kChunkTokens > R.w_lo_min;
+      Chunk ch;
+      // Read before the issue below: its page lookup shares the LDS reads'
+      // wait counter.
+      if (mine) read_chunk(ring_base + (k % ns) * kSlotBytes, ro, ch);
+      if (k + ahead < len) {
+        issue_rows_chunk(p, Ld, ring + ((k + ahead) % ns) * kSlotBytes, rs, mask, lane);
+        if (k + ahead + 1 < len) rows_pages(p, B, c + kChunkTokens * (ahead + 1), Ld);
+      }
+      if (mine) {
+        Int8Ops ops{ch};
+        compute_rows<kF16Q>(R, L, c, ops, qb, qlo, scl, st);
+      }
+    }
+    const int ng = R.two ? 2 : 1;
+    if (kp > 1) {
+      __syncthreads();  // every wave is done with the slots
+      if (part > 0 && R.has_rows) merge_store(merge_area(lds, wave - (mask + 1)), lane, st, ng);
+      __syncthreads();
+      if (part == 0 && R.has_rows) {
+        for (int j = 1; j < kp; ++j) {
+          const char* a = merge_area(lds, (j - 1) * (mask + 1) + rs);
+#pragma unroll
+          for (int i = 0; i < 2; ++i)
+            if (i < ng) merge_add(a, lane, st[i], i);
+        }
+      }
+    }
+    if (part == 0 && R.has_rows) {
+      epilogue(p, U0, L[0], st[0]);
+      if (R.two) epilogue(p, U1, L[1], st[1]);
+    }
+  }
+}
+
+}  // namespace
+
+hipError_t launch_rows_kernel(const AttnParams& p, dim3 grid, bool windowed, bool q_f16,
+                              hipStream_t stream) {
+  const dim3 block(kRowWaves * 64);
+  if (windowed) {
+    if (q_f16) hipLaunchKernelGGL((attn_fwd_rows<true, true>), grid, block, 0, stream, p);
+    else hipLaunchKernelGGL((attn_fwd_rows<true, false>), grid, block, 0, stream, p);
+  } else {
+    if (q_f16) hipLaunchKernelGGL((attn_fwd_rows<false, true>), grid, block, 0, stream, p);
+    else hipLaunchKernelGGL((attn_fwd_rows<false, false>), grid, block, 0, stream, p);
+  }
+  return hipGetLastError();
+}
+
+int32_t rows_block_tokens(int32_t group) {
+  return group >= kBlockRows ? 1 : kBlockRows / group;
+}
+
+}  // namespace pa

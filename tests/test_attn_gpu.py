@@ -160,6 +160,49 @@ def test_grid_forced_splits(case):
     check_case(case, num_splits=5)
 
 
+# Single-split launches with 64-row tiles run the row-block kernel (8 waves
+# share each key chunk; blocks of 256 / G tokens; short requests split their
+# keys over the waves and merge). These cases cover every row-set / key-part
+# shape (1 x 8, 2 x 4, 4 x 2, 8 x 1), GQA groups that do not divide a block's
+# 32-row wave sets, windows, non-causal rows, fp16 q and other page shapes.
+GRID_ROWS = [
+    Case("rows-mixed", q_lens=[1, 3, 10, 20, 64, 100, 300, 1],
+         seq_lens=[5000, 40, 900, 20, 64, 3000, 1500, 33], seed=50),
+    Case("rows-g1", q_lens=[300, 1, 50], seq_lens=[2000, 700, 50], Hq=8, Hkv=8, seed=51),
+    Case("rows-g8", q_lens=[70, 2, 33], seq_lens=[500, 4000, 33], Hq=16, Hkv=2, seed=52),
+    Case("rows-g6", q_lens=[90, 5], seq_lens=[700, 2500], Hq=12, Hkv=2, seed=53),
+    Case("rows-window", q_lens=[200, 7, 40], seq_lens=[900, 3000, 1200], window=64, seed=54),
+    Case("rows-window-long", q_lens=[130, 17], seq_lens=[5000, 800], window=1000, seed=55),
+    Case("rows-noncausal", q_lens=[100, 2], seq_lens=[400, 50], causal=False, seed=56),
+    Case("rows-window-noncausal", q_lens=[80, 4], seq_lens=[2000, 300], window=100,
+         causal=False, seed=57),
+    Case("rows-fp16q", q_lens=[65, 1], seq_lens=[800, 1000], q_dtype=torch.float16, seed=58),
+    Case("rows-bs64", q_lens=[48, 1], seq_lens=[1000, 3333], block_size=64, seed=59),
+    Case("rows-bs528", q_lens=[40], seq_lens=[1200], Hq=8, Hkv=2, block_size=528, seed=60),
+    Case("rows-hnd", q_lens=[33, 1], seq_lens=[600, 90], layout="HND", seed=61),
+    Case("rows-padded", q_lens=[20, 1], seq_lens=[20, 70], pad_tokens=7, seed=62),
+    Case("rows-short", q_lens=[17, 1], seq_lens=[17, 1], seed=63),
+]
+
+
+@pytest.mark.parametrize("case", GRID_ROWS, ids=lambda c: c.name)
+def test_row_blocks(case):
+    check_case(case, num_splits=1)
+
+
+def test_row_blocks_deterministic_and_op():
+    c = Case("rows-op", q_lens=[100, 1, 9], seq_lens=[2000, 5000, 300], seed=64,
+             num_splits=1)
+    b = materialize(c, DEV)
+    o1, l1 = run_capi(b)
+    o2, l2 = run_capi(b)
+    assert torch.equal(o1.view(torch.int16), o2.view(torch.int16))
+    assert torch.equal(l1, l2)
+    o_op = run_op(b)
+    o_capi, _ = run_capi(b, with_lse=False)
+    assert torch.equal(o_op.view(torch.int16), o_capi.view(torch.int16))
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
 def test_out_dtypes(dtype):
     c = Case("out-" + str(dtype), q_lens=[1, 2], seq_lens=[500, 70], Hq=8, Hkv=2, seed=30)
