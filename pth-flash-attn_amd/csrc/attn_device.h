@@ -85,10 +85,17 @@ __device__ __forceinline__ SwapPair swap_halves(float x) {
   const uint32_t r0 = r[0], r1 = r[1];
   return {__builtin_bit_cast(float, r0), __builtin_bit_cast(float, r1)};
 }
+// max of two floats as the bare instruction: fmaxf would first quiet the
+// operands that come from a cross-lane move (2 extra instructions each).
+__device__ __forceinline__ float max_raw(float a, float b) {
+  float r;
+  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
 __device__ __forceinline__ float xor_max(float x) {
   const SwapPair a = swap_rows16(x);
-  const SwapPair b = swap_halves(fmaxf(a.a, a.b));
-  return fmaxf(b.a, b.b);
+  const SwapPair b = swap_halves(max_raw(a.a, a.b));
+  return max_raw(b.a, b.b);
 }
 __device__ __forceinline__ float xor_sum(float x) {
   const SwapPair a = swap_rows16(x);

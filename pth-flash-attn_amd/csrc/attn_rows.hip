@@ -364,12 +364,15 @@ __device__ __forceinline__ void compute_rows(const RowSet& R, const Lanes (&L)[2
 //   K: [sub 2][j 4][lane 64] x 16 B  -- bf16 K[16 sub + (l % 16)][32 (l / 16) + 8 j ..]
 //   V: [j 8][lane 64] x 16 B         -- bf16 V[tv(e)][8 (l % 16) + j], e = 0..7
 // Wave w converts K operand (sub, j) = (w / 4, w % 4) and V column j = w.
+// A wide block advances two chunks per barrier step: step s computes chunks
+// 2s, 2s + 1, converts chunks 2s + 2, 2s + 3 and issues the loads of chunks
+// 2s + 6, 2s + 7 (so four chunks are in flight), into the int8 slots that
+// chunks 2s - 2, 2s - 1 left.
 constexpr int kWideSlots = 8;  // int8 chunk slots of a wide block
-constexpr int kWideAhead = 3;  // int8 chunks in flight beyond the one being converted
 constexpr int kCopyBytes = 16384;
+constexpr int kCopies = 4;     // bf16 copies: the pair computed and the pair converted
 constexpr int kCopyBase = kWideSlots * kSlotBytes;
-static_assert(kCopyBase + 2 * kCopyBytes <= kRowSlots * kSlotBytes, "wide-block LDS");
-static_assert(kWideAhead + 2 <= kWideSlots, "a refilled slot must be two chunks old");
+static_assert(kCopyBase + kCopies * kCopyBytes <= kRowSlots * kSlotBytes, "wide-block LDS");
 
 __device__ __forceinline__ uint32_t ds_read_i8(uint32_t a) {
   uint32_t v;
@@ -523,11 +526,63 @@ __device__ __forceinline__ void merge_add(const char* a, int lane, State& st, in
   st.m = M;
 }
 
-// The chunk loop of a wide block. Step k: wait for this wave's loads of
-// chunk k + 1, barrier (chunk k + 1 is in LDS, the bf16 copy of chunk k is
-// complete, every wave is done with the copy of chunk k - 1), refill the
-// int8 slot of chunk k - 4, convert this wave's share of chunk k + 1 into
-// the copy chunk k - 1 used, compute chunk k from its copy.
+// Pages of the two chunks at key c (4 groups of 16 keys), looked up one step
+// ahead of their loads.
+struct PairPages {
+  int32_t page[4], slot0[4];
+};
+
+__device__ __forceinline__ void pair_pages(const AttnParams& p, const Block& B, int64_t bt0, int c,
+                                           PairPages& pp) {
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int c16 = c + 16 * q;
+    pp.page[q] = 0;
+    pp.slot0[q] = 0;
+    if (c16 < B.ld_hi && c16 + 16 > B.ld_lo) {
+      const int blk = static_cast<int>(p.bs_div.div(c16));
+      pp.slot0[q] = c16 - blk * static_cast<int>(p.bs_div.d);
+      pp.page[q] = ld_ro(p.block_table, bt0 + blk);
+    }
+  }
+}
+
+// Wave w's loads of chunk h (0, 1) of a pair: load d = w of the chunk (K rows
+// 8w .. for w < 4, V rows 8(w - 4) .. otherwise), and wave 0 also the scales.
+// The selection is wave-uniform arithmetic, no branch but the scales'.
+__device__ __forceinline__ void issue_wide(const AttnParams& p, const RowLoader& Ld,
+                                           const PairPages& pp, int h, char* slot, int wave,
+                                           int lane) {
+  const int q = wave & 3;
+  const bool isv = wave >= 4;
+  // Group 2h + (q >> 1), selected without indexing (a run-time index would
+  // move the array to memory).
+  const bool hi = (q >> 1) != 0;
+  const int32_t page = h == 0 ? (hi ? pp.page[1] : pp.page[0]) : (hi ? pp.page[3] : pp.page[2]);
+  const int32_t slot0 = h == 0 ? (hi ? pp.slot0[1] : pp.slot0[0]) : (hi ? pp.slot0[3] : pp.slot0[2]);
+  const char* base = p.cell_base + static_cast<uint64_t>(static_cast<uint32_t>(page)) * p.cell_block +
+                     static_cast<uint32_t>(slot0) * p.cell_slot;
+  // Rows 8 (q & 1) + lane / 8 of the group, K or V: the lane's K offset of
+  // the first row plus uniform terms (no selection between the offsets).
+  const uint32_t off = Ld.off_k[0] + (isv ? p.cell_off[1] - p.cell_off[0] : 0u) +
+                       static_cast<uint32_t>(q & 1) * 8u * p.cell_slot;
+  dma16(base + off, slot + (isv ? kSlotV : kSlotK) + 1024 * q);
+  if (wave == 0) {
+    const int32_t pa = h == 0 ? pp.page[0] : pp.page[2], pb = h == 0 ? pp.page[1] : pp.page[3];
+    const int32_t sa = h == 0 ? pp.slot0[0] : pp.slot0[2], sb = h == 0 ? pp.slot0[1] : pp.slot0[3];
+    const char* b0 = p.cell_base + static_cast<uint64_t>(static_cast<uint32_t>(pa)) * p.cell_block +
+                     static_cast<uint32_t>(sa) * p.cell_slot;
+    const char* b1 = p.cell_base + static_cast<uint64_t>(static_cast<uint32_t>(pb)) * p.cell_block +
+                     static_cast<uint32_t>(sb) * p.cell_slot;
+    dma4(((lane >> 4) & 1 ? b1 : b0) + Ld.off_s, slot + kSlotScale);
+  }
+}
+
+// The chunk loop of a wide block, two chunks per step (see kWideSlots).
+// Before step s the copies of chunks 2s, 2s + 1 are complete. Step s: wait
+// for this wave's loads of chunks 2s + 2, 2s + 3; barrier (they are in LDS,
+// every wave is done with step s - 1); issue chunks 2s + 6, 2s + 7; convert
+// this wave's shares of chunks 2s + 2, 2s + 3; compute chunks 2s, 2s + 1.
 template <bool kF16Q>
 __device__ __forceinline__ void wide_block(const AttnParams& p, const Block& B, const RowSet& R,
                                            const Lanes (&L)[2], RowLoader& Ld,
@@ -537,41 +592,52 @@ __device__ __forceinline__ void wide_block(const AttnParams& p, const Block& B, 
                                            int wave, int lane) {
   const int len = B.n_chunks;
   if (len == 0) return;
-  constexpr int mask = kRowWaves - 1;
-  const int nload = rows_chunk_loads(mask, wave);
+  const int nload = wave == 0 ? 2 : 1;
   const uint32_t copy0 = lds_base + kCopyBase;
-  rows_pages(p, B, B.c_begin, Ld);
-  for (int i = 0; i <= kWideAhead && i < len; ++i) {
-    issue_rows_chunk(p, Ld, lds + i * kSlotBytes, wave, mask, lane);
-    if (i + 1 < len) rows_pages(p, B, B.c_begin + kChunkTokens * (i + 1), Ld);
+  auto slot_of = [&](int k) { return (k % kWideSlots) * kSlotBytes; };
+  auto copy_of = [&](int k) { return (k % kCopies) * kCopyBytes; };
+  auto chunk_key = [&](int k) { return B.c_begin + kChunkTokens * k; };
+  PairPages pp;
+  for (int k = 0; k < 6 && k < len; k += 2) {
+    pair_pages(p, B, Ld.bt0, chunk_key(k), pp);
+    issue_wide(p, Ld, pp, 0, lds + slot_of(k), wave, lane);
+    if (k + 1 < len) issue_wide(p, Ld, pp, 1, lds + slot_of(k + 1), wave, lane);
   }
+  if (6 < len) pair_pages(p, B, Ld.bt0, chunk_key(6), pp);
+  // Chunks 0, 1 landed: at most the loads of chunks 2 .. 5 outstanding.
   {
-    const int last = kWideAhead < len - 1 ? kWideAhead : len - 1;
-    wait_vmcnt_dyn(nload * last);
+    const int issued = len < 6 ? len : 6;
+    const int younger = issued - 2 > 0 ? issued - 2 : 0;
+    wait_vmcnt_dyn(nload * younger);
   }
   wg_barrier();
-  convert_share(lds_base, copy0, cvo, wave, lane);
-  for (int k = 0; k < len; ++k) {
-    if (k + 1 < len) {
-      const int last = k + kWideAhead < len - 1 ? k + kWideAhead : len - 1;
-      wait_vmcnt_dyn(nload * (last - k - 1));
+  convert_share(lds_base + slot_of(0), copy0 + copy_of(0), cvo, wave, lane);
+  if (1 < len) convert_share(lds_base + slot_of(1), copy0 + copy_of(1), cvo, wave, lane);
+  for (int k = 0; k < len; k += 2) {
+    if (k + 2 < len) {
+      // Issued so far: chunks up to min(k + 5, len - 1); k + 2, k + 3 must land.
+      const int last = k + 5 < len - 1 ? k + 5 : len - 1;
+      const int younger = last - (k + 3) > 0 ? last - (k + 3) : 0;
+      wait_vmcnt_dyn(nload * younger);
     }
     wait_lgkmcnt0();  // this wave's copy writes
     wg_barrier();
-    if (k + 1 + kWideAhead < len)
-      issue_rows_chunk(p, Ld, lds + ((k + 1 + kWideAhead) % kWideSlots) * kSlotBytes, wave, mask,
-                       lane);
-    if (k + 1 < len)
-      convert_share(lds_base + ((k + 1) % kWideSlots) * kSlotBytes,
-                    copy0 + ((k + 1) & 1) * kCopyBytes, cvo, wave, lane);
-    const int c = B.c_begin + kChunkTokens * k;
-    if (R.has_rows && c <= R.w_hi_max && c + kChunkTokens > R.w_lo_min) {
-      CopyOps ops(copy0 + (k & 1) * kCopyBytes, lds_base + (k % kWideSlots) * kSlotBytes + ro.s,
-                  lane);
-      compute_rows<kF16Q>(R, L, c, ops, qb, qlo, scl, st);
+    if (k + 6 < len) {
+      issue_wide(p, Ld, pp, 0, lds + slot_of(k + 6), wave, lane);
+      if (k + 7 < len) issue_wide(p, Ld, pp, 1, lds + slot_of(k + 7), wave, lane);
     }
-    if (k + 2 + kWideAhead < len)
-      rows_pages(p, B, B.c_begin + kChunkTokens * (k + 2 + kWideAhead), Ld);
+    if (k + 2 < len) convert_share(lds_base + slot_of(k + 2), copy0 + copy_of(k + 2), cvo, wave, lane);
+    if (k + 3 < len) convert_share(lds_base + slot_of(k + 3), copy0 + copy_of(k + 3), cvo, wave, lane);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int kk = k + h;
+      const int c = chunk_key(kk);
+      if (kk < len && R.has_rows && c <= R.w_hi_max && c + kChunkTokens > R.w_lo_min) {
+        CopyOps ops(copy0 + copy_of(kk), lds_base + slot_of(kk) + ro.s, lane);
+        compute_rows<kF16Q>(R, L, c, ops, qb, qlo, scl, st);
+      }
+    }
+    if (k + 8 < len) pair_pages(p, B, Ld.bt0, chunk_key(k + 8), pp);
   }
 }
 
