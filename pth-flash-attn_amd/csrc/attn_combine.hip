@@ -1,5 +1,5 @@
 // attn_combine.hip -- merge of the split-KV partials (flash-decoding
-// combine) for D = 128.
+// combine), head size D = 64, 128 or 256.
 //
 // Split s of a query row left o_s (fp32, normalised) and lse_s = m_s +
 // log2(l_s) (log2 units; -inf when the split saw no key). The exact output is
@@ -15,8 +15,8 @@
 // (token, head) row: wave 0 alone, or, for a row with more than 64 splits,
 // all 4 (wave w merges the 64-split blocks w, w + 4, ... and wave 0 merges
 // the 4 results in a fixed order). Otherwise one wave per row.
-// Lane l owns columns 2 l and 2 l + 1, so a split's row is one coalesced
-// 512-byte read. Lane s loads lse_s (64 splits per instruction);
+// Lane l owns columns [l NC, (l + 1) NC), NC = D / 64, so a split's row is
+// one coalesced 4 D-byte read. Lane s loads lse_s (64 splits per instruction);
 // the weights are broadcast with readlane and the o loads of 16 splits are
 // issued before their fused multiply-adds. When the launcher
 // passes the request lengths, only the splits the attention kernel wrote for
@@ -31,6 +31,9 @@ namespace {
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 
 constexpr float kNegInf = -__builtin_inff();
 constexpr int kBatch = 16;
@@ -89,21 +92,38 @@ __device__ __forceinline__ int row_live_splits(const CombineParams& c, int r, in
   return live;
 }
 
+// NC consecutive fp32 columns at p (4 NC-byte aligned).
+template <int NC>
+__device__ __forceinline__ void load_cols(const char* p, float (&x)[NC]) {
+  if constexpr (NC == 4) {
+    const f32x4 t = *reinterpret_cast<const f32x4*>(p);
+    x[0] = t[0]; x[1] = t[1]; x[2] = t[2]; x[3] = t[3];
+  } else if constexpr (NC == 2) {
+    const f32x2 t = *reinterpret_cast<const f32x2*>(p);
+    x[0] = t[0]; x[1] = t[1];
+  } else {
+    x[0] = *reinterpret_cast<const float*>(p);
+  }
+}
+
 // Merges splits of the 64-split blocks first, first + step, ... of row
 // (tok, head): the maximum M of their log2-LSEs and, relative to it, this
-// lane's two numerator columns and the (wave-summed) denominator.
+// lane's NC numerator columns and the (wave-summed) denominator.
+template <int NC>
 __device__ __forceinline__ void merge_blocks(const CombineParams& c, int64_t tok, int head, int S,
-                                             int first, int step, int lane, float& M, f32x2& num,
-                                             float& den) {
+                                             int first, int step, int lane, float& M,
+                                             float (&num)[NC], float& den) {
   const char* lse_row = c.ws_lse + tok * c.s_wl_tok + static_cast<int64_t>(head) * c.s_wl_head;
-  const char* o_row = c.ws_o + tok * c.s_wo_tok + static_cast<int64_t>(head) * c.s_wo_head + 8 * lane;
+  const char* o_row =
+      c.ws_o + tok * c.s_wo_tok + static_cast<int64_t>(head) * c.s_wo_head + 4 * NC * lane;
   M = kNegInf;
   for (int s = 64 * first + lane; s < S; s += 64 * step) {
     const float x = *reinterpret_cast<const float*>(lse_row + s * c.s_wl_split);
     M = x > M ? x : M;  // -inf and NaN never win
   }
   M = wave_max(M);
-  num = (f32x2){0.0f, 0.0f};
+#pragma unroll
+  for (int i = 0; i < NC; ++i) num[i] = 0.0f;
   den = 0.0f;
   if (!(M > kNegInf)) return;
   float den_l = 0.0f;
@@ -115,21 +135,25 @@ __device__ __forceinline__ void merge_blocks(const CombineParams& c, int64_t tok
     const int n = S - s0 < 64 ? S - s0 : 64;
     for (int e0 = 0; e0 < n; e0 += kBatch) {
       float w[kBatch];
-      f32x2 ov[kBatch];
+      float ov[kBatch][NC];
 #pragma unroll
       for (int k = 0; k < kBatch; ++k) {
         const int e = e0 + k;
         w[k] = e < n ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(
                                                       __builtin_bit_cast(int, w_l), e))
                      : 0.0f;
-        ov[k] = w[k] > 0.0f ? *reinterpret_cast<const f32x2*>(o_row + (s0 + e) * c.s_wo_split)
-                            : (f32x2){0.0f, 0.0f};
+        if (w[k] > 0.0f) {
+          load_cols<NC>(o_row + (s0 + e) * c.s_wo_split, ov[k]);
+        } else {
+#pragma unroll
+          for (int i = 0; i < NC; ++i) ov[k][i] = 0.0f;
+        }
       }
 #pragma unroll
       for (int k = 0; k < kBatch; ++k) {
         if (w[k] > 0.0f) {
-          num[0] = fmaf(w[k], ov[k][0], num[0]);
-          num[1] = fmaf(w[k], ov[k][1], num[1]);
+#pragma unroll
+          for (int i = 0; i < NC; ++i) num[i] = fmaf(w[k], ov[k][i], num[i]);
         }
       }
     }
@@ -137,17 +161,43 @@ __device__ __forceinline__ void merge_blocks(const CombineParams& c, int64_t tok
   den = wave_sum(den_l);
 }
 
+template <int NC>
 __device__ __forceinline__ void write_row(const CombineParams& c, int64_t tok, int head, float M,
-                                          f32x2 num, float den, int lane) {
+                                          const float (&num)[NC], float den, int lane) {
   const float inv = den > 0.0f ? 1.0f / den : 0.0f;
-  const float r0 = num[0] * inv, r1 = num[1] * inv;
+  float r[NC];
+#pragma unroll
+  for (int i = 0; i < NC; ++i) r[i] = num[i] * inv;
   char* dst = c.out + tok * c.s_out_tok + static_cast<int64_t>(head) * c.s_out_head;
   if (c.out_dtype == PTH_ATTN_BF16) {
-    *reinterpret_cast<bf16x2*>(dst + 4 * lane) = __builtin_convertvector((f32x2){r0, r1}, bf16x2);
+    if constexpr (NC == 4) {
+      *reinterpret_cast<bf16x4*>(dst + 8 * lane) =
+          __builtin_convertvector((f32x4){r[0], r[1], r[2], r[3]}, bf16x4);
+    } else if constexpr (NC == 2) {
+      *reinterpret_cast<bf16x2*>(dst + 4 * lane) =
+          __builtin_convertvector((f32x2){r[0], r[1]}, bf16x2);
+    } else {
+      *reinterpret_cast<__bf16*>(dst + 2 * lane) = static_cast<__bf16>(r[0]);
+    }
   } else if (c.out_dtype == PTH_ATTN_F16) {
-    *reinterpret_cast<f16x2*>(dst + 4 * lane) = (f16x2){static_cast<_Float16>(r0), static_cast<_Float16>(r1)};
+    if constexpr (NC == 4) {
+      *reinterpret_cast<f16x4*>(dst + 8 * lane) =
+          (f16x4){static_cast<_Float16>(r[0]), static_cast<_Float16>(r[1]),
+                  static_cast<_Float16>(r[2]), static_cast<_Float16>(r[3])};
+    } else if constexpr (NC == 2) {
+      *reinterpret_cast<f16x2*>(dst + 4 * lane) =
+          (f16x2){static_cast<_Float16>(r[0]), static_cast<_Float16>(r[1])};
+    } else {
+      *reinterpret_cast<_Float16*>(dst + 2 * lane) = static_cast<_Float16>(r[0]);
+    }
   } else {
-    *reinterpret_cast<f32x2*>(dst + 8 * lane) = (f32x2){r0, r1};
+    if constexpr (NC == 4) {
+      *reinterpret_cast<f32x4*>(dst + 16 * lane) = (f32x4){r[0], r[1], r[2], r[3]};
+    } else if constexpr (NC == 2) {
+      *reinterpret_cast<f32x2*>(dst + 8 * lane) = (f32x2){r[0], r[1]};
+    } else {
+      *reinterpret_cast<float*>(dst + 4 * lane) = r[0];
+    }
   }
   if (c.lse_out != nullptr && lane == 0) {
     float* lo = reinterpret_cast<float*>(reinterpret_cast<char*>(c.lse_out) + tok * c.s_lo_tok +
@@ -160,10 +210,12 @@ __device__ __forceinline__ void write_row(const CombineParams& c, int64_t tok, i
 // work-group together; the others by wave 0 alone.
 constexpr int kSharedRowSplits = 64;
 
-__global__ __launch_bounds__(256) void combine_d128(const CombineParams c) {
+template <int D>
+__global__ __launch_bounds__(256) void combine_splits(const CombineParams c) {
+  constexpr int NC = D / 64;  // columns per lane
   __shared__ int row_splits;
   __shared__ float part_m[kWaves], part_den[kWaves];
-  __shared__ f32x2 part_num[kWaves][64];
+  __shared__ float part_num[kWaves][NC][64];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   if (!c.shared_rows) {  // one row per wave, whatever its split count
@@ -176,9 +228,9 @@ __global__ __launch_bounds__(256) void combine_d128(const CombineParams c) {
     const int S = c.seq_lens != nullptr ? row_live_splits(c, r, tok, head, lane) : c.num_splits;
     if (c.seq_lens != nullptr && S == 1) return;  // written to out by the attention kernel
     float M, den;
-    f32x2 num;
-    merge_blocks(c, tok, head, S, 0, 1, lane, M, num, den);
-    write_row(c, tok, head, M, num, den, lane);
+    float num[NC];
+    merge_blocks<NC>(c, tok, head, S, 0, 1, lane, M, num, den);
+    write_row<NC>(c, tok, head, M, num, den, lane);
     return;
   }
   const int64_t row = blockIdx.x;
@@ -196,41 +248,43 @@ __global__ __launch_bounds__(256) void combine_d128(const CombineParams c) {
   __syncthreads();
   const int S = row_splits;
   float M, den;
-  f32x2 num;
+  float num[NC];
   if (S <= kSharedRowSplits) {
     if (wave != 0 || S == 0) return;
-    merge_blocks(c, tok, head, S, 0, 1, lane, M, num, den);
-    write_row(c, tok, head, M, num, den, lane);
+    merge_blocks<NC>(c, tok, head, S, 0, 1, lane, M, num, den);
+    write_row<NC>(c, tok, head, M, num, den, lane);
     return;
   }
   // The 4 waves take the 64-split blocks in turn; wave 0 merges their
   // results in a fixed order.
-  merge_blocks(c, tok, head, S, wave, kWaves, lane, M, num, den);
+  merge_blocks<NC>(c, tok, head, S, wave, kWaves, lane, M, num, den);
   if (lane == 0) {
     part_m[wave] = M;
     part_den[wave] = den;
   }
-  part_num[wave][lane] = num;
+#pragma unroll
+  for (int i = 0; i < NC; ++i) part_num[wave][i][lane] = num[i];
   __syncthreads();
   if (wave != 0) return;
   float Mg = kNegInf;
 #pragma unroll
   for (int w = 0; w < kWaves; ++w) Mg = part_m[w] > Mg ? part_m[w] : Mg;
-  f32x2 ng = {0.0f, 0.0f};
+  float ng[NC];
+#pragma unroll
+  for (int i = 0; i < NC; ++i) ng[i] = 0.0f;
   float dg = 0.0f;
   if (Mg > kNegInf) {
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) {
       if (part_m[w] > kNegInf) {
         const float a = __builtin_amdgcn_exp2f(part_m[w] - Mg);
-        const f32x2 pn = part_num[w][lane];
-        ng[0] = fmaf(a, pn[0], ng[0]);
-        ng[1] = fmaf(a, pn[1], ng[1]);
+#pragma unroll
+        for (int i = 0; i < NC; ++i) ng[i] = fmaf(a, part_num[w][i][lane], ng[i]);
         dg = fmaf(a, part_den[w], dg);
       }
     }
   }
-  write_row(c, tok, head, Mg, ng, dg, lane);
+  write_row<NC>(c, tok, head, Mg, ng, dg, lane);
 }
 
 // -inf into the log2-LSE slot of every split s >= live of every query row
@@ -265,7 +319,16 @@ hipError_t launch_fill_unused_splits(const CombineParams& c, hipStream_t stream)
 hipError_t launch_combine_kernel(const CombineParams& c, hipStream_t stream) {
   const int64_t rows = static_cast<int64_t>(c.num_tokens) * c.num_q_heads;
   const unsigned blocks = static_cast<unsigned>(c.shared_rows ? rows : (rows + kWaves - 1) / kWaves);
-  hipLaunchKernelGGL(combine_d128, dim3(blocks), dim3(kWaves * 64), 0, stream, c);
+  switch (c.head_size) {
+    case 64:
+      hipLaunchKernelGGL(combine_splits<64>, dim3(blocks), dim3(kWaves * 64), 0, stream, c);
+      break;
+    case 256:
+      hipLaunchKernelGGL(combine_splits<256>, dim3(blocks), dim3(kWaves * 64), 0, stream, c);
+      break;
+    default:
+      hipLaunchKernelGGL(combine_splits<128>, dim3(blocks), dim3(kWaves * 64), 0, stream, c);
+  }
   return hipGetLastError();
 }
 

@@ -214,6 +214,109 @@ __device__ __forceinline__ void make_unit(const AttnParams& p, const RowTile& t,
   U.n_chunks = U.c_begin < U.ld_hi ? (U.ld_hi - U.c_begin + kChunkTokens - 1) / kChunkTokens : 0;
 }
 
+// The work of one wave, in the order it runs it. Two partitions:
+//   * num_splits == 1: units are (request, row tile, KV-head unit), whole
+//     key ranges; wave w of the grid's W waves takes units w, w + W, ...,
+//     of a table derived on the device from query_start_loc and seq_lens
+//     (a prefix sum over requests, 64 per wave instruction).
+//   * num_splits > 1 (kStream): the chunk-stream partition of
+//     attn_geometry.h. Work-group b runs positions [b per, (b + 1) per);
+//     wave w of it takes KV-head unit 8 g + w of each group g it meets, so
+//     the 8 waves of a work-group read the 8 adjacent heads of the same keys
+//     (their cells share cache lines), and every split but a stream's last
+//     is exactly per chunks long.
+template <bool kWindow, bool kStream>
+struct Work {
+  // num_splits == 1
+  int r0 = -64;  // first request of the cursor's 64-request window
+  int u0 = 0;    // units before the window
+  int u1 = 0;    // units through the window
+  int incl = 0;  // per lane: inclusive prefix within the window
+  int next_u = 0;
+  int stride = 0;
+  // num_splits > 1
+  StreamCursor sc;
+  StreamDesc d;
+  int64_t pos = 0, stop = 0, per = 1;
+  int wg = 0, wave = 0;
+
+  __device__ __forceinline__ void init(const AttnParams& p, int lane) {
+    const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
+    if constexpr (kStream) {
+      d = StreamDesc{p.qsl, p.seq_lens, p.num_reqs, p.bq, kWindow ? p.window : 0,
+                     kWindow ? p.causal : 1, p.n_hg, static_cast<int32_t>(gridDim.x),
+                     p.num_splits};
+      int64_t total;
+      per = stream_per(d, lane, total);
+      wg = blockIdx.x;
+      wave = w;
+      pos = static_cast<int64_t>(wg) * per;
+      stop = pos + per < total ? pos + per : total;
+    } else {
+      next_u = blockIdx.x * kGroupUnits + w;
+      stride = gridDim.x * kGroupUnits;
+    }
+  }
+
+  // The next unit of this wave (possibly without rows or keys); false at the
+  // end of its work.
+  __device__ __forceinline__ bool next(const AttnParams& p, int lane, Unit& U) {
+    if constexpr (kStream) {
+      while (pos < stop) {
+        StreamPos sp;
+        if (!stream_locate(d, sc, pos, lane, sp)) {
+          pos = stop;
+          return false;
+        }
+        const int c0 = static_cast<int>(pos - sp.c0);
+        const int64_t end = sp.c0 + sp.n < stop ? sp.c0 + sp.n : stop;
+        const int c1 = static_cast<int>(end - sp.c0);
+        pos = end;
+        const int hu = sp.hg * kGroupUnits + wave;
+        if (hu >= p.n_hu) continue;  // the group has fewer units than waves
+        int first, live;
+        stream_splits(sp.c0, sp.n, per, first, live);
+        make_unit<kWindow>(p, sp.t, hu, sp.cb + kChunkTokens * c0, sp.cb + kChunkTokens * c1,
+                           wg - first, live, U);
+        return true;
+      }
+      return false;
+    } else {
+      const int window = kWindow ? p.window : 0;
+      const bool causal = kWindow ? (p.causal != 0) : true;
+      const int u = next_u;
+      next_u += stride;
+      while (u >= u1) {
+        r0 += 64;
+        u0 = u1;
+        if (r0 >= p.num_reqs) return false;
+        const int r = r0 + lane;
+        const int units =
+            r < p.num_reqs ? request_row_tiles(p.qsl[r + 1] - p.qsl[r], p.bq) * p.n_hu : 0;
+        int x = units;
+#pragma unroll
+        for (int dd = 1; dd < 64; dd <<= 1) {
+          const int v = __shfl_up(x, dd);
+          if (lane >= dd) x += v;
+        }
+        incl = x;
+        u1 = u0 + __builtin_amdgcn_readlane(x, 63);
+      }
+      const int local = u - u0;
+      const int j = static_cast<int>(__popcll(__ballot(incl <= local)));
+      const int req = r0 + j;
+      const int u_loc = local - (j > 0 ? __builtin_amdgcn_readlane(incl, j - 1) : 0);
+      const int q_start = ld_ro(p.qsl, req);
+      const int q_len = ld_ro(p.qsl, req + 1) - q_start;
+      const int seq_len = ld_ro(p.seq_lens, req);
+      const RowTile t = request_tile(req, q_start, q_len, seq_len, p.bq, u_loc / p.n_hu);
+      make_unit<kWindow>(p, t, u_loc % p.n_hu, tile_chunk_base(t, window),
+                         range_end(t, window, causal), 0, 1, U);
+      return true;
+    }
+  }
+};
+
 // Per-lane view of the unit's rows: lane l holds row row0 + (l % 16).
 struct Lanes {
   int r16, g;
@@ -248,22 +351,38 @@ __device__ __forceinline__ Lanes unit_lanes(const AttnParams& p, const Unit& U, 
   return L;
 }
 
-// Q^T as the B operand of QK: qb[j] holds Q[row][32 g + 8 j .. + 8] in bf16
+// Head-size geometry of the per-lane layout (the comment at the top of
+// attn_fwd.hip describes D = 128). Lane (r, g) holds, per key, bytes
+// [g D/4, (g + 1) D/4) of K (QK MFMA j takes bytes 8j .. 8j + 8 of them);
+// per V run, bytes [r D/16, (r + 1) D/16) of 8 keys (PV MFMA j takes byte
+// j); and O[row][(D/16)(4g + i) + j] in o[j][i], i.e. the D/4 contiguous
+// output columns [g D/4, (g + 1) D/4).
+template <int D>
+struct HeadDim {
+  static_assert(D == 64 || D == 128 || D == 256, "head size 64, 128 or 256");
+  static constexpr int kQK = D / 32;  // QK MFMAs per 16 keys (Q operands per lane)
+  static constexpr int kPV = D / 16;  // PV MFMAs (output column groups)
+  static constexpr int kCols = D / 4; // output columns per lane
+};
+
+// Q^T as the B operand of QK: qb[j] holds Q[row][g D/4 + 8 j .. + 8] in bf16
 // (and, for an fp16 q, qlo[j] the exact remainder q - bf16(q)). load_q_raw
-// issues the four 16-byte loads; q_operands converts them.
-__device__ __forceinline__ void load_q_raw(const AttnParams& p, const Lanes& L, u32x4 (&raw)[4]) {
+// issues the 16-byte loads; q_operands converts them.
+template <int D = 128>
+__device__ __forceinline__ void load_q_raw(const AttnParams& p, const Lanes& L,
+                                           u32x4 (&raw)[HeadDim<D>::kQK]) {
   const char* qrow = p.q + L.qtok * p.s_q_tok + static_cast<int64_t>(L.head) * p.s_q_head;
 #pragma unroll
-  for (int j = 0; j < 4; ++j)
-    raw[j] = L.vrow ? *reinterpret_cast<const u32x4*>(qrow + 2 * (32 * L.g + 8 * j))
+  for (int j = 0; j < HeadDim<D>::kQK; ++j)
+    raw[j] = L.vrow ? *reinterpret_cast<const u32x4*>(qrow + 2 * (HeadDim<D>::kCols * L.g + 8 * j))
                     : (u32x4){0u, 0u, 0u, 0u};
 }
 
-template <bool kF16Q>
-__device__ __forceinline__ void q_operands(const u32x4 (&raw)[4], bf16x8 (&qb)[4],
-                                           bf16x8 (&qlo)[4]) {
+template <bool kF16Q, int N>
+__device__ __forceinline__ void q_operands(const u32x4 (&raw)[N], bf16x8 (&qb)[N],
+                                           bf16x8 (&qlo)[N]) {
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
+  for (int j = 0; j < N; ++j) {
     if constexpr (kF16Q) {
       // fp16 q = hi + lo with hi = bf16(q), lo = bf16(q - hi): exact, since an
       // fp16 significand has 11 bits and each bf16 holds 8.
@@ -285,24 +404,28 @@ __device__ __forceinline__ void q_operands(const u32x4 (&raw)[4], bf16x8 (&qb)[4
   }
 }
 
-template <bool kF16Q>
-__device__ __forceinline__ void load_q(const AttnParams& p, const Lanes& L, bf16x8 (&qb)[4],
-                                       bf16x8 (&qlo)[4]) {
-  u32x4 raw[4];
-  load_q_raw(p, L, raw);
+template <bool kF16Q, int D = 128>
+__device__ __forceinline__ void load_q(const AttnParams& p, const Lanes& L,
+                                       bf16x8 (&qb)[HeadDim<D>::kQK],
+                                       bf16x8 (&qlo)[HeadDim<D>::kQK]) {
+  u32x4 raw[HeadDim<D>::kQK];
+  load_q_raw<D>(p, L, raw);
   q_operands<kF16Q>(raw, qb, qlo);
 }
 
 // Online-softmax state of one wave's 16 rows.
-struct State {
-  f32x4 o[8];  // o[j][i] = O[row][32 g + 8 i + j] (unnormalised)
-  float m;     // running max (log2 units), equal in the 4 lanes of a row
-  float l;     // this lane's part of the running sum
+template <int D>
+struct StateT {
+  f32x4 o[HeadDim<D>::kPV];  // o[j][i] = O[row][(D/16)(4g + i) + j] (unnormalised)
+  float m;                   // running max (log2 units), equal in the 4 lanes of a row
+  float l;                   // this lane's part of the running sum
 };
+using State = StateT<128>;
 
-__device__ __forceinline__ void state_reset(State& st) {
+template <int D>
+__device__ __forceinline__ void state_reset(StateT<D>& st) {
 #pragma unroll
-  for (int j = 0; j < 8; ++j) st.o[j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  for (int j = 0; j < HeadDim<D>::kPV; ++j) st.o[j] = (f32x4){0.f, 0.f, 0.f, 0.f};
   st.m = kNegInf;
   st.l = 0.0f;
 }
@@ -310,19 +433,33 @@ __device__ __forceinline__ void state_reset(State& st) {
 // One 32-key chunk starting at key c: S = K Q^T, mask, online softmax, O += V P.
 // The reference max m only moves when a row's chunk max exceeds it by more
 // than kRescaleSlack (log2 units): p = 2^(s - m) then stays <= 2^8, exact
-// in fp32 accumulation and bf16 hi + lo, and the 32 multiplies of the O
-// rescale are skipped for every chunk where no row's max grew that much (all
-// chunks but a few at the start of a long row). The result is the same
-// softmax: the final normalisation divides the common factor out. A row's
-// first chunk with a visible key always sets m.
+// in fp32 accumulation and bf16 hi + lo, and the O rescale is skipped for
+// every chunk where no row's max grew that much (all chunks but a few at
+// the start of a long row). The result is the same softmax: the final
+// normalisation divides the common factor out. A row's first chunk with a
+// visible key always sets m.
 constexpr float kRescaleSlack = 8.0f;
 
-template <bool kF16Q>
-__device__ __forceinline__ void compute_chunk(const Unit& U, const Lanes& L, int c,
-                                              const Chunk& ch, const bf16x8 (&qb)[4],
-                                              const bf16x8 (&qlo)[4], float scl,
-                                              State& st) {
-  const float sc1 = ch.sc * scl;
+// The operands of a chunk in registers as the D = 128 paged kernels load
+// them (Chunk); ops.k(sub, j) / ops.v(j) give the bf16 K and V operands and
+// ops.sc the lane's scale.
+struct ChunkOps {
+  const Chunk& ch;
+  __device__ __forceinline__ float sc() const { return ch.sc; }
+  __device__ __forceinline__ bf16x8 k(int sub, int j) const {
+    const u32x4& w = ch.k[sub][j >> 1];
+    return (j & 1) ? i8x8_to_bf16(w[2], w[3]) : i8x8_to_bf16(w[0], w[1]);
+  }
+  __device__ __forceinline__ bf16x8 v(int j) const { return column_to_bf16(ch.v, j); }
+};
+
+template <int D, bool kF16Q, class Ops>
+__device__ __forceinline__ void compute_chunk_t(const Unit& U, const Lanes& L, int c,
+                                                const Ops& ops,
+                                                const bf16x8 (&qb)[HeadDim<D>::kQK],
+                                                const bf16x8 (&qlo)[HeadDim<D>::kQK], float scl,
+                                                StateT<D>& st) {
+  const float sc1 = ops.sc() * scl;
   const float ks[8] = {row_bcast<0>(sc1), row_bcast<1>(sc1), row_bcast<2>(sc1),
                        row_bcast<3>(sc1), row_bcast<4>(sc1), row_bcast<5>(sc1),
                        row_bcast<6>(sc1), row_bcast<7>(sc1)};
@@ -336,9 +473,8 @@ __device__ __forceinline__ void compute_chunk(const Unit& U, const Lanes& L, int
   for (int sub = 0; sub < 2; ++sub) {
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const u32x4& w = ch.k[sub][j >> 1];
-      const bf16x8 a = (j & 1) ? i8x8_to_bf16(w[2], w[3]) : i8x8_to_bf16(w[0], w[1]);
+    for (int j = 0; j < HeadDim<D>::kQK; ++j) {
+      const bf16x8 a = ops.k(sub, j);
       acc = mfma(a, qb[j], acc);
       if constexpr (kF16Q) acc = mfma(a, qlo[j], acc);
     }
@@ -367,7 +503,7 @@ __device__ __forceinline__ void compute_chunk(const Unit& U, const Lanes& L, int
     const float alpha = grow && !fresh ? __builtin_amdgcn_exp2f(-mx) : 1.0f;
     st.l *= alpha;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) st.o[j] *= alpha;
+    for (int j = 0; j < HeadDim<D>::kPV; ++j) st.o[j] *= alpha;
     const float shift = grow ? mx : 0.0f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) t[e] -= shift;
@@ -399,31 +535,43 @@ __device__ __forceinline__ void compute_chunk(const Unit& U, const Lanes& L, int
     p_lo[e + 1] = lw[1];
   }
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const bf16x8 vcol = column_to_bf16(ch.v, j);
+  for (int j = 0; j < HeadDim<D>::kPV; ++j) {
+    const bf16x8 vcol = ops.v(j);
     st.o[j] = mfma(vcol, p_hi, st.o[j]);
     st.o[j] = mfma(vcol, p_lo, st.o[j]);
   }
 }
 
+template <bool kF16Q>
+__device__ __forceinline__ void compute_chunk(const Unit& U, const Lanes& L, int c,
+                                              const Chunk& ch, const bf16x8 (&qb)[4],
+                                              const bf16x8 (&qlo)[4], float scl,
+                                              State& st) {
+  compute_chunk_t<128, kF16Q>(U, L, c, ChunkOps{ch}, qb, qlo, scl, st);
+}
+
 // A finished unit's result, held in registers until it is stored.
-struct Finished {
-  float res[32];  // res[8 i + j] = normalised O[row][32 g + 8 i + j]
-  float lse2;     // log2-sum-exp of the row, -inf without a visible key
+template <int D>
+struct FinishedT {
+  float res[HeadDim<D>::kCols];  // res[(D/16) i + j] = normalised O[row][g D/4 + (D/16) i + j]
+  float lse2;                    // log2-sum-exp of the row, -inf without a visible key
   int64_t qtok;
   int head, g;
   bool vrow;
   int s, live;
 };
+using Finished = FinishedT<128>;
 
-__device__ __forceinline__ void finish(const Unit& U, const Lanes& L, const State& st,
-                                       Finished& f) {
+template <int D>
+__device__ __forceinline__ void finish(const Unit& U, const Lanes& L, const StateT<D>& st,
+                                       FinishedT<D>& f) {
+  constexpr int kPV = HeadDim<D>::kPV;
   const float l_tot = xor_sum(st.l);
   const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
 #pragma unroll
-  for (int j = 0; j < 8; ++j)
+  for (int j = 0; j < kPV; ++j)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) f.res[8 * i + j] = st.o[j][i] * inv;
+    for (int i = 0; i < 4; ++i) f.res[kPV * i + j] = st.o[j][i] * inv;
   f.lse2 = l_tot > 0.0f ? st.m + __builtin_amdgcn_logf(l_tot) : kNegInf;
   f.qtok = L.qtok;
   f.head = L.head;
@@ -443,23 +591,27 @@ __device__ __forceinline__ bool direct_out(const AttnParams& p, int live) {
 // it is issued (the lanes without a row are masked off, never the whole
 // wave: row 0 of a unit always exists), so that the waits of the chunk
 // pipeline can count past them.
+template <int D = 128>
 __device__ __forceinline__ int stores_per_unit(const AttnParams& p, int live) {
-  if (!direct_out(p, live)) return 9;
-  return (p.out_dtype == PTH_ATTN_F32 ? 8 : 4) + (p.lse_out != nullptr ? 1 : 0);
+  constexpr int kCols = HeadDim<D>::kCols;
+  if (!direct_out(p, live)) return kCols / 4 + 1;
+  return (p.out_dtype == PTH_ATTN_F32 ? kCols / 4 : kCols / 8) + (p.lse_out != nullptr ? 1 : 0);
 }
 
 // Stores a finished unit: out (and lse_out, natural log) or its split's
 // partials. Split slots a row does not use are left untouched here
 // (fill_unused_splits writes them when a caller needs them).
-__device__ __forceinline__ void store_finished(const AttnParams& p, const Finished& f) {
+template <int D>
+__device__ __forceinline__ void store_finished(const AttnParams& p, const FinishedT<D>& f) {
+  constexpr int kCols = HeadDim<D>::kCols;
   if (!f.vrow) return;
   const int g = f.g;
   const int64_t head = f.head;
   if (!direct_out(p, f.live)) {
     char* dst = reinterpret_cast<char*>(p.ws_o) + f.s * p.s_wo_split + f.qtok * p.s_wo_tok +
-                head * p.s_wo_head + 4 * 32 * g;
+                head * p.s_wo_head + 4 * kCols * g;
 #pragma unroll
-    for (int k = 0; k < 8; ++k)
+    for (int k = 0; k < kCols / 4; ++k)
       *reinterpret_cast<f32x4*>(dst + 16 * k) =
           (f32x4){f.res[4 * k], f.res[4 * k + 1], f.res[4 * k + 2], f.res[4 * k + 3]};
     // The 4 lanes of a row hold the same lse2 and store it to the same place.
@@ -469,9 +621,9 @@ __device__ __forceinline__ void store_finished(const AttnParams& p, const Finish
   }
   char* dst = p.out + f.qtok * p.s_out_tok + head * p.s_out_head;
   if (p.out_dtype == PTH_ATTN_BF16) {
-    dst += 2 * 32 * g;
+    dst += 2 * kCols * g;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
+    for (int k = 0; k < kCols / 8; ++k) {
       bf16x8 v;
 #pragma unroll
       for (int e = 0; e < 8; e += 2) {
@@ -482,18 +634,18 @@ __device__ __forceinline__ void store_finished(const AttnParams& p, const Finish
       *reinterpret_cast<bf16x8*>(dst + 16 * k) = v;
     }
   } else if (p.out_dtype == PTH_ATTN_F16) {
-    dst += 2 * 32 * g;
+    dst += 2 * kCols * g;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
+    for (int k = 0; k < kCols / 8; ++k) {
       f16x8 v;
 #pragma unroll
       for (int e = 0; e < 8; ++e) v[e] = static_cast<_Float16>(f.res[8 * k + e]);
       *reinterpret_cast<f16x8*>(dst + 16 * k) = v;
     }
   } else {
-    dst += 4 * 32 * g;
+    dst += 4 * kCols * g;
 #pragma unroll
-    for (int k = 0; k < 8; ++k)
+    for (int k = 0; k < kCols / 4; ++k)
       *reinterpret_cast<f32x4*>(dst + 16 * k) =
           (f32x4){f.res[4 * k], f.res[4 * k + 1], f.res[4 * k + 2], f.res[4 * k + 3]};
   }
@@ -504,9 +656,10 @@ __device__ __forceinline__ void store_finished(const AttnParams& p, const Finish
   }
 }
 
+template <int D>
 __device__ __forceinline__ void epilogue(const AttnParams& p, const Unit& U, const Lanes& L,
-                                         const State& st) {
-  Finished f;
+                                         const StateT<D>& st) {
+  FinishedT<D> f;
   finish(U, L, st, f);
   store_finished(p, f);
 }

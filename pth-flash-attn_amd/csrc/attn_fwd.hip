@@ -52,109 +52,6 @@
 namespace pa {
 namespace {
 
-// The work of one wave, in the order it runs it. Two partitions:
-//   * num_splits == 1: units are (request, row tile, KV-head unit), whole
-//     key ranges; wave w of the grid's W waves takes units w, w + W, ...,
-//     of a table derived on the device from query_start_loc and seq_lens
-//     (a prefix sum over requests, 64 per wave instruction).
-//   * num_splits > 1 (kStream): the chunk-stream partition of
-//     attn_geometry.h. Work-group b runs positions [b per, (b + 1) per);
-//     wave w of it takes KV-head unit 8 g + w of each group g it meets, so
-//     the 8 waves of a work-group read the 8 adjacent heads of the same keys
-//     (their cells share cache lines), and every split but a stream's last
-//     is exactly per chunks long.
-template <bool kWindow, bool kStream>
-struct Work {
-  // num_splits == 1
-  int r0 = -64;  // first request of the cursor's 64-request window
-  int u0 = 0;    // units before the window
-  int u1 = 0;    // units through the window
-  int incl = 0;  // per lane: inclusive prefix within the window
-  int next_u = 0;
-  int stride = 0;
-  // num_splits > 1
-  StreamCursor sc;
-  StreamDesc d;
-  int64_t pos = 0, stop = 0, per = 1;
-  int wg = 0, wave = 0;
-
-  __device__ __forceinline__ void init(const AttnParams& p, int lane) {
-    const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
-    if constexpr (kStream) {
-      d = StreamDesc{p.qsl, p.seq_lens, p.num_reqs, p.bq, kWindow ? p.window : 0,
-                     kWindow ? p.causal : 1, p.n_hg, static_cast<int32_t>(gridDim.x),
-                     p.num_splits};
-      int64_t total;
-      per = stream_per(d, lane, total);
-      wg = blockIdx.x;
-      wave = w;
-      pos = static_cast<int64_t>(wg) * per;
-      stop = pos + per < total ? pos + per : total;
-    } else {
-      next_u = blockIdx.x * kGroupUnits + w;
-      stride = gridDim.x * kGroupUnits;
-    }
-  }
-
-  // The next unit of this wave (possibly without rows or keys); false at the
-  // end of its work.
-  __device__ __forceinline__ bool next(const AttnParams& p, int lane, Unit& U) {
-    if constexpr (kStream) {
-      while (pos < stop) {
-        StreamPos sp;
-        if (!stream_locate(d, sc, pos, lane, sp)) {
-          pos = stop;
-          return false;
-        }
-        const int c0 = static_cast<int>(pos - sp.c0);
-        const int64_t end = sp.c0 + sp.n < stop ? sp.c0 + sp.n : stop;
-        const int c1 = static_cast<int>(end - sp.c0);
-        pos = end;
-        const int hu = sp.hg * kGroupUnits + wave;
-        if (hu >= p.n_hu) continue;  // the group has fewer units than waves
-        int first, live;
-        stream_splits(sp.c0, sp.n, per, first, live);
-        make_unit<kWindow>(p, sp.t, hu, sp.cb + kChunkTokens * c0, sp.cb + kChunkTokens * c1,
-                           wg - first, live, U);
-        return true;
-      }
-      return false;
-    } else {
-      const int window = kWindow ? p.window : 0;
-      const bool causal = kWindow ? (p.causal != 0) : true;
-      const int u = next_u;
-      next_u += stride;
-      while (u >= u1) {
-        r0 += 64;
-        u0 = u1;
-        if (r0 >= p.num_reqs) return false;
-        const int r = r0 + lane;
-        const int units =
-            r < p.num_reqs ? request_row_tiles(p.qsl[r + 1] - p.qsl[r], p.bq) * p.n_hu : 0;
-        int x = units;
-#pragma unroll
-        for (int dd = 1; dd < 64; dd <<= 1) {
-          const int v = __shfl_up(x, dd);
-          if (lane >= dd) x += v;
-        }
-        incl = x;
-        u1 = u0 + __builtin_amdgcn_readlane(x, 63);
-      }
-      const int local = u - u0;
-      const int j = static_cast<int>(__popcll(__ballot(incl <= local)));
-      const int req = r0 + j;
-      const int u_loc = local - (j > 0 ? __builtin_amdgcn_readlane(incl, j - 1) : 0);
-      const int q_start = ld_ro(p.qsl, req);
-      const int q_len = ld_ro(p.qsl, req + 1) - q_start;
-      const int seq_len = ld_ro(p.seq_lens, req);
-      const RowTile t = request_tile(req, q_start, q_len, seq_len, p.bq, u_loc / p.n_hu);
-      make_unit<kWindow>(p, t, u_loc % p.n_hu, tile_chunk_base(t, window),
-                         range_end(t, window, causal), 0, 1, U);
-      return true;
-    }
-  }
-};
-
 // ---------------------------------------------------------------------------
 // Paged kernel (block size a multiple of 16): the 16-key halves of a chunk
 // each lie in one page. A producer walks this wave's chunk sequence -- all
@@ -458,81 +355,6 @@ void attn_fwd_paged_reg(const AttnParams p) {
   }
 }
 
-// ---------------------------------------------------------------------------
-// Generic kernel (any block size): one page lookup per key, loads straight to
-// registers, the next chunk in flight while the current one is computed.
-template <bool kWindow>
-__device__ __forceinline__ void load_chunk_generic(const AttnParams& p, const Unit& U,
-                                                   const Lanes& L, int c, Chunk& ch) {
-  const int BS = static_cast<int>(p.bs_div.d);
-  const int32_t* bt = p.block_table + static_cast<int64_t>(U.t.req) * p.bt_stride;
-  const int r16 = L.r16, g = L.g;
-#pragma unroll
-  for (int sub = 0; sub < 2; ++sub) {
-    const int tk = c + 16 * sub + r16;
-    u32x4 k0 = {0u, 0u, 0u, 0u}, k1 = {0u, 0u, 0u, 0u};
-    if (tk >= U.ld_lo && tk < U.ld_hi) {
-      const int blk = static_cast<int>(p.bs_div.div(tk));
-      const char* kp = at(p.k, bt[blk], tk - blk * BS, U.kvh) + 32 * g;
-      k0 = *reinterpret_cast<const u32x4_a4*>(kp);
-      k1 = *reinterpret_cast<const u32x4_a4*>(kp + 16);
-    }
-    ch.k[sub][0] = k0;
-    ch.k[sub][1] = k1;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int tv = c + 16 * sub + 4 * g + i;
-      u32x2 vv = {0u, 0u};
-      if (tv >= U.ld_lo && tv < U.ld_hi) {
-        const int blk = static_cast<int>(p.bs_div.div(tv));
-        vv = *reinterpret_cast<const u32x2_a4*>(at(p.v, bt[blk], tv - blk * BS, U.kvh) + 8 * r16);
-      }
-      ch.v[4 * sub + i] = vv;
-    }
-  }
-  const int e = r16 & 7;
-  const int ts = c + 16 * (e >> 2) + 4 * g + (e & 3);
-  float scv = 0.0f;
-  if (ts >= U.ld_lo && ts < U.ld_hi) {
-    const int blk = static_cast<int>(p.bs_div.div(ts));
-    scv = *reinterpret_cast<const float*>(at(r16 < 8 ? p.ks : p.vs, bt[blk], ts - blk * BS, U.kvh));
-  }
-  ch.sc = scv;
-}
-
-template <bool kWindow, bool kStream, bool kF16Q>
-__global__ __launch_bounds__(kFwdWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
-void attn_fwd_generic(const AttnParams p) {
-  const int lane = threadIdx.x & 63;
-  const float scl = scale_factor(lane & 15, p.scale_log2);
-  Work<kWindow, kStream> work;
-  work.init(p, lane);
-  Unit U;
-  while (work.next(p, lane, U)) {
-    if (!U.has_rows) continue;
-    const Lanes L = unit_lanes<kWindow>(p, U, lane);
-    State st;
-    state_reset(st);
-    if (U.n_chunks > 0) {
-      bf16x8 qb[4], qlo[4];
-      load_q<kF16Q>(p, L, qb, qlo);
-      Chunk ca, cb;
-      int k = 0;
-      load_chunk_generic<kWindow>(p, U, L, U.c_begin, ca);
-      while (true) {
-        const int c = U.c_begin + kChunkTokens * k;
-        if (k + 1 < U.n_chunks) load_chunk_generic<kWindow>(p, U, L, c + kChunkTokens, cb);
-        compute_chunk<kF16Q>(U, L, c, ca, qb, qlo, scl, st);
-        if (++k >= U.n_chunks) break;
-        if (k + 1 < U.n_chunks) load_chunk_generic<kWindow>(p, U, L, c + 2 * kChunkTokens, ca);
-        compute_chunk<kF16Q>(U, L, c + kChunkTokens, cb, qb, qlo, scl, st);
-        if (++k >= U.n_chunks) break;
-      }
-    }
-    epilogue(p, U, L, st);
-  }
-}
-
 // Chunks in flight per wave on the paged path (LDS slots per wave).
 constexpr int kPagedInFlight = PA_PAGED_INFLIGHT;
 
@@ -551,30 +373,22 @@ hipError_t launch_paged(const AttnParams& p, dim3 grid, hipStream_t stream) {
   }
   return hipGetLastError();
 }
-template <bool W, bool St, bool F>
-hipError_t launch_generic(const AttnParams& p, dim3 grid, hipStream_t stream) {
-  hipLaunchKernelGGL((attn_fwd_generic<W, St, F>), grid, dim3(kFwdWaves * 64), 0, stream, p);
-  return hipGetLastError();
-}
-
 template <bool W, bool St>
-hipError_t launch_variant(const AttnParams& p, dim3 grid, bool paged16, bool q_f16,
-                          hipStream_t stream) {
-  if (paged16) return q_f16 ? launch_paged<W, St, true>(p, grid, stream)
-                            : launch_paged<W, St, false>(p, grid, stream);
-  return q_f16 ? launch_generic<W, St, true>(p, grid, stream)
-               : launch_generic<W, St, false>(p, grid, stream);
+hipError_t launch_variant(const AttnParams& p, dim3 grid, bool q_f16, hipStream_t stream) {
+  return q_f16 ? launch_paged<W, St, true>(p, grid, stream)
+               : launch_paged<W, St, false>(p, grid, stream);
 }
 
 }  // namespace
 
 hipError_t launch_fwd_kernel(const AttnParams& p, dim3 grid, bool windowed,
                              bool paged16, bool q_f16, hipStream_t stream) {
+  if (!paged16) return launch_generic_kernel(p, grid, windowed, q_f16, 128, stream);
   const bool stream_split = p.num_splits > 1;
-  if (windowed) return stream_split ? launch_variant<true, true>(p, grid, paged16, q_f16, stream)
-                                    : launch_variant<true, false>(p, grid, paged16, q_f16, stream);
-  return stream_split ? launch_variant<false, true>(p, grid, paged16, q_f16, stream)
-                      : launch_variant<false, false>(p, grid, paged16, q_f16, stream);
+  if (windowed) return stream_split ? launch_variant<true, true>(p, grid, q_f16, stream)
+                                    : launch_variant<true, false>(p, grid, q_f16, stream);
+  return stream_split ? launch_variant<false, true>(p, grid, q_f16, stream)
+                      : launch_variant<false, false>(p, grid, q_f16, stream);
 }
 
 }  // namespace pa

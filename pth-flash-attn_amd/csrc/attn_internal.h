@@ -85,6 +85,7 @@ struct CombineParams {
   int32_t num_tokens;
   int32_t num_q_heads;
   int32_t num_splits;
+  int32_t head_size;  // 64, 128 or 256
   // When seq_lens is non-NULL the combine reads only the splits the
   // attention kernel wrote for the row (the stream partition of
   // attn_geometry.h for these lengths and launch constants) and skips rows
@@ -123,6 +124,10 @@ int32_t launch_combine(const PthAttnCombineArgs& c, hipStream_t stream,
 int32_t resident_workgroups();
 hipError_t launch_fwd_kernel(const AttnParams& p, dim3 grid, bool windowed,
                              bool paged16, bool q_f16, hipStream_t stream);
+// The register-load kernel for any block size and cache strides, head size
+// 64, 128 or 256 (attn_generic.hip); windowed / non-causal at 128 only.
+hipError_t launch_generic_kernel(const AttnParams& p, dim3 grid, bool windowed, bool q_f16,
+                                 int head_size, hipStream_t stream);
 // The row-block kernel (num_splits == 1, paged cell caches) and the query
 // tokens of one of its blocks for GQA group `group`.
 hipError_t launch_rows_kernel(const AttnParams& p, dim3 grid, bool windowed, bool q_f16,

@@ -135,9 +135,9 @@ int32_t launch_attention(const PthAttnArgs& a, int32_t loader,
              "out_dtype must be PTH_ATTN_F32, PTH_ATTN_F16 or PTH_ATTN_BF16");
   PA_REQUIRE(a.head_size == 64 || a.head_size == 128 || a.head_size == 256,
              "head_size must be 64, 128 or 256");
-  PA_REQUIRE(a.head_size == 128,
-             "head_size " + std::to_string(a.head_size) +
-                 " has no gfx950 kernel in this library (D = 128 only)");
+  PA_REQUIRE(a.head_size == 128 || (a.window == 0 && a.causal == 1),
+             "sliding-window and non-causal attention need head size D = 128, got " +
+                 std::to_string(a.head_size));
   PA_REQUIRE(a.num_kv_heads >= 1 && a.num_q_heads >= a.num_kv_heads &&
                  a.num_q_heads % a.num_kv_heads == 0,
              "num_q_heads must be a positive multiple of num_kv_heads");
@@ -259,9 +259,14 @@ int32_t launch_attention(const PthAttnArgs& a, int32_t loader,
   // Row tiles of 64 rows (the planner's prefill and wide-verify plans) on a
   // single split: the row-block kernel, whose 8 waves share each key chunk
   // (one work-group per CU, never more than there are blocks).
-  const bool row_blocks = a.num_splits == 1 && paged16 && rows >= 64;
+  // Head sizes 64 and 256: the register-load kernel (any block size).
+  const bool d128 = a.head_size == 128;
+  const bool row_blocks = d128 && a.num_splits == 1 && paged16 && rows >= 64;
   hipError_t err;
-  if (row_blocks) {
+  if (!d128) {
+    const dim3 grid(static_cast<unsigned>(wg));
+    err = launch_generic_kernel(p, grid, false, a.q_dtype == PTH_ATTN_F16, a.head_size, stream);
+  } else if (row_blocks) {
     const int64_t blocks =
         (static_cast<int64_t>(a.num_tokens) / p.blk_tok + a.num_reqs) * a.num_kv_heads;
     PA_REQUIRE(blocks < 0x7fffffff, "the block table exceeds 2^31 - 1 blocks");
@@ -272,7 +277,8 @@ int32_t launch_attention(const PthAttnArgs& a, int32_t loader,
     err = launch_fwd_kernel(p, grid, windowed, paged16, a.q_dtype == PTH_ATTN_F16, stream);
   }
   if (err != hipSuccess) {
-    return fail(PTH_ATTN_ECUDA, std::string("attention launch (D=128, rows=") +
+    return fail(PTH_ATTN_ECUDA, std::string("attention launch (D=") +
+                                    std::to_string(a.head_size) + ", rows=" +
                                     std::to_string(rows) + "): " +
                                     hipGetErrorString(err));
   }
@@ -287,6 +293,7 @@ int32_t launch_attention(const PthAttnArgs& a, int32_t loader,
     f.num_tokens = a.num_tokens;
     f.num_q_heads = a.num_q_heads;
     f.num_splits = a.num_splits;
+    f.head_size = a.head_size;
     stream_fields(a, f);
     const hipError_t e2 = launch_fill_unused_splits(f, stream);
     if (e2 != hipSuccess)
@@ -299,9 +306,8 @@ int32_t launch_combine(const PthAttnCombineArgs& c, hipStream_t stream,
                        float* lse_out, int64_t lse_stride_token,
                        int64_t lse_stride_head, const PthAttnArgs* split_source) {
   clear_error();
-  PA_REQUIRE(c.head_size == 128,
-             "head_size " + std::to_string(c.head_size) +
-                 " has no gfx950 combine in this library (D = 128 only)");
+  PA_REQUIRE(c.head_size == 64 || c.head_size == 128 || c.head_size == 256,
+             "head_size must be 64, 128 or 256");
   PA_REQUIRE(c.out_dtype == PTH_ATTN_F32 || c.out_dtype == PTH_ATTN_F16 ||
                  c.out_dtype == PTH_ATTN_BF16,
              "out_dtype must be PTH_ATTN_F32, PTH_ATTN_F16 or PTH_ATTN_BF16");
@@ -311,17 +317,19 @@ int32_t launch_combine(const PthAttnCombineArgs& c, hipStream_t stream,
   PA_REQUIRE(c.num_q_heads >= 1, "num_q_heads must be >= 1");
   PA_REQUIRE(c.ws_o && c.ws_lse && c.out && c.query_start_loc,
              "ws_o, ws_lse, out and query_start_loc must be non-NULL");
-  PA_REQUIRE(aligned(c.ws_o, 8) && c.ws_o_stride_split % 8 == 0 &&
-                 c.ws_o_stride_token % 8 == 0 && c.ws_o_stride_head % 8 == 0,
-             "ws_o base and byte strides must be 8-B aligned");
+  // Each lane reads (and writes) D / 64 consecutive columns.
+  const int64_t cols = c.head_size / 64;
+  PA_REQUIRE(aligned(c.ws_o, 4 * cols) && c.ws_o_stride_split % (4 * cols) == 0 &&
+                 c.ws_o_stride_token % (4 * cols) == 0 && c.ws_o_stride_head % (4 * cols) == 0,
+             "ws_o base and byte strides must be aligned to D / 64 floats");
   PA_REQUIRE(aligned(c.ws_lse, 4) && c.ws_lse_stride_split % 4 == 0 &&
                  c.ws_lse_stride_token % 4 == 0 &&
                  c.ws_lse_stride_head % 4 == 0,
              "ws_lse base and byte strides must be 4-B aligned");
-  const int64_t elem = c.out_dtype == PTH_ATTN_F32 ? 8 : 4;
+  const int64_t elem = (c.out_dtype == PTH_ATTN_F32 ? 4 : 2) * cols;
   PA_REQUIRE(aligned(c.out, elem) && c.out_stride_token % elem == 0 &&
                  c.out_stride_head % elem == 0,
-             "out base and byte strides must be aligned to two elements");
+             "out base and byte strides must be aligned to D / 64 elements");
   CombineParams p{};
   p.ws_o = reinterpret_cast<const char*>(c.ws_o);
   p.s_wo_split = c.ws_o_stride_split;
@@ -343,6 +351,7 @@ int32_t launch_combine(const PthAttnCombineArgs& c, hipStream_t stream,
   p.num_tokens = c.num_tokens;
   p.num_q_heads = c.num_q_heads;
   p.num_splits = c.num_splits;
+  p.head_size = c.head_size;
   if (split_source != nullptr) stream_fields(*split_source, p);
   const int64_t rows = static_cast<int64_t>(c.num_tokens) * c.num_q_heads;
   p.shared_rows = c.num_splits > 64 && rows < 4 * static_cast<int64_t>(resident_workgroups());
@@ -414,7 +423,8 @@ const char* pth_attn_last_error(void) { return pa::last_error(); }
 int32_t pth_attn_tiling(int32_t head_size, int32_t bq, int32_t group,
                         int32_t* n_tile, int32_t* sub_tile, int32_t* wn) {
   pa::clear_error();
-  PA_REQUIRE(head_size == 128, "head_size must be 128 (the only D built)");
+  PA_REQUIRE(head_size == 64 || head_size == 128 || head_size == 256,
+             "head_size must be 64, 128 or 256");
   PA_REQUIRE(bq >= 1 && group >= 1, "bq and group must be >= 1");
   PA_REQUIRE(n_tile && sub_tile && wn, "output pointers must be non-NULL");
   PA_REQUIRE(static_cast<int64_t>(bq) * group <= 64, "bq * G exceeds 64 rows");

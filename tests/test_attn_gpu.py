@@ -203,6 +203,46 @@ def test_row_blocks_deterministic_and_op():
     assert torch.equal(o_op.view(torch.int16), o_capi.view(torch.int16))
 
 
+# Head sizes 64 and 256 (the reference op's other instantiations): the
+# register-load kernel and the combine at D / 64 columns per lane. Causal
+# only, as in the reference (windows and non-causal need D = 128).
+GRID_D = [
+    Case("d64-decode", q_lens=[1, 1, 1], seq_lens=[1, 300, 2049], Hq=8, Hkv=2, D=64, seed=70),
+    Case("d64-verify", q_lens=[4, 2], seq_lens=[700, 129], D=64, seed=71),
+    Case("d64-prefill", q_lens=[37, 100], seq_lens=[37, 500], Hq=8, Hkv=2, D=64, seed=72),
+    Case("d64-hnd", q_lens=[1, 4], seq_lens=[513, 90], D=64, layout="HND", seed=73),
+    Case("d64-padded", q_lens=[1, 3], seq_lens=[50, 400], Hq=8, Hkv=2, D=64, pad_tokens=3,
+         seed=74),
+    Case("d256-decode-g6", q_lens=[1, 1], seq_lens=[5000, 17], Hq=12, Hkv=2, D=256, seed=75),
+    Case("d256-verify-g6", q_lens=[5, 3], seq_lens=[2000, 99], Hq=12, Hkv=2, D=256, seed=76),
+    Case("d256-prefill", q_lens=[64, 10], seq_lens=[300, 10], Hq=12, Hkv=2, D=256, seed=77),
+    Case("d256-bs7", q_lens=[3, 1], seq_lens=[100, 9], Hq=8, Hkv=2, D=256, block_size=7, seed=78),
+    Case("d256-fp16q", q_lens=[1, 4], seq_lens=[300, 65], Hq=8, Hkv=2, D=256,
+         q_dtype=torch.float16, seed=79),
+]
+
+
+@pytest.mark.parametrize("case", GRID_D, ids=lambda c: c.name)
+def test_head_sizes(case):
+    check_case(case)
+
+
+@pytest.mark.parametrize("case", [GRID_D[0], GRID_D[2], GRID_D[5], GRID_D[7]],
+                         ids=lambda c: c.name)
+@pytest.mark.parametrize("S", [1, 5])
+def test_head_sizes_forced_splits(case, S):
+    check_case(case, num_splits=S)
+
+
+@pytest.mark.parametrize("D", [64, 256])
+def test_head_sizes_op_equals_capi(D):
+    c = Case(f"op-d{D}", q_lens=[1, 4, 1], seq_lens=[3000, 400, 77], Hq=8, Hkv=2, D=D, seed=80)
+    b = materialize(c, DEV)
+    o_op = run_op(b)
+    o_capi, _ = run_capi(b, with_lse=False)
+    assert torch.equal(o_op.view(torch.int16), o_capi.view(torch.int16))
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
 def test_out_dtypes(dtype):
     c = Case("out-" + str(dtype), q_lens=[1, 2], seq_lens=[500, 70], Hq=8, Hkv=2, seed=30)

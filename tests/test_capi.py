@@ -111,7 +111,8 @@ def _valid_args(D: int = 128, splits: int = 1):
 @pytest.mark.parametrize(("mutate", "msg"), [
     (lambda a: setattr(a, "abi_version", 1), "abi_version 1 != library ABI 2"),
     (lambda a: setattr(a, "struct_bytes", 344), "struct_bytes 344 != sizeof(PthAttnArgs) 352"),
-    (lambda a: setattr(a, "head_size", 64), "D = 128 only"),
+    (lambda a: (setattr(a, "head_size", 64), setattr(a, "window", 16)), "need head size D = 128"),
+    (lambda a: (setattr(a, "head_size", 256), setattr(a, "causal", 0)), "need head size D = 128"),
     (lambda a: setattr(a, "head_size", 96), "head_size"),
     (lambda a: setattr(a, "num_splits", 0), "num_splits must be >= 1"),
     (lambda a: setattr(a, "softmax_scale", float("nan")), "softmax_scale"),
@@ -161,8 +162,9 @@ def test_combine_rejects_invalid_arguments(lib):
     qsl = torch.tensor([0, 1, 2], dtype=torch.int32)
     c = capi.combine_args(ws_o=ws_o, ws_lse=ws_l, out=out, query_start_loc=qsl, num_reqs=2,
                           num_splits=S)
-    c.head_size = 64
+    c.head_size = 96
     assert lib.combine(c) == capi.PTH_ATTN_EINVAL
+    assert "head_size" in lib.last_error()
     c.head_size = 128
     c.num_splits = 0
     assert lib.combine(c) == capi.PTH_ATTN_EINVAL
@@ -177,8 +179,10 @@ def test_tiling(lib):
     assert lib.tiling(128, 4, 4) == (64, 32, 1)
     assert lib.tiling(128, 16, 4) == (64, 32, 4)
     assert lib.tiling(128, 10, 6) == (64, 32, 4)
+    assert lib.tiling(64, 4, 4) == (64, 32, 1)
+    assert lib.tiling(256, 16, 4) == (64, 32, 4)
     with pytest.raises(RuntimeError, match="head_size"):
-        lib.tiling(256, 1, 4)
+        lib.tiling(96, 1, 4)
     with pytest.raises(RuntimeError, match="64 rows"):
         lib.tiling(128, 17, 4)
 
