@@ -151,6 +151,38 @@ typedef struct PthAttnCombineArgs {
   int32_t num_splits;
 } PthAttnCombineArgs;
 
+/* Arguments of the int8 cache writer (pth_attn_write_kv). No counterpart in
+ * the reference's ABI: the reference relies on vLLM's Triton writer
+ * triton_reshape_and_cache_flash_per_token_head_quant (vLLM 0.31.0; its call
+ * site and mirror: python/pth_testing/reference.py:76-103, 301-307), which
+ * is not available on ROCm here. Token t of key/value goes to slot
+ * slot_mapping[t] of the cache (page slot / block_size, in-page slot
+ * slot % block_size); a negative slot skips the token. The cache views are
+ * the four of PthAttnArgs (byte strides; the vLLM cell shares them). */
+typedef struct PthAttnWriteArgs {
+  int32_t abi_version;  /* = PTH_ATTN_ABI_VERSION */
+  int32_t struct_bytes; /* = sizeof(PthAttnWriteArgs) */
+
+  const void* key;   /* [num_tokens, num_kv_heads, head_size] */
+  const void* value; /* [num_tokens, num_kv_heads, head_size] */
+  int64_t key_stride_token; /* bytes */
+  int64_t key_stride_head;
+  int64_t value_stride_token;
+  int64_t value_stride_head;
+  int32_t kv_dtype; /* PTH_ATTN_F32, PTH_ATTN_F16 or PTH_ATTN_BF16 */
+  int32_t num_tokens;
+  int32_t num_kv_heads;
+  int32_t head_size; /* 64, 128 or 256 */
+  const int64_t* slot_mapping; /* [num_tokens] */
+
+  PthAttnStream k_cache; /* int8 [num_blocks, block_size, num_kv_heads, head_size] */
+  PthAttnStream v_cache;
+  PthAttnStream k_scale; /* fp32 [num_blocks, block_size, num_kv_heads] */
+  PthAttnStream v_scale;
+  int32_t block_size;
+  int32_t num_blocks;
+} PthAttnWriteArgs;
+
 /* Loader choice of pth_attn_attention_ex. Reference: attn_capi.h:32-39.
  * loader: 0 = default, 1 = separate streams (the only loader of this
  * library; 0 and 1 are the same), 2 = whole cell (not built: EINVAL). */
@@ -165,6 +197,8 @@ int32_t pth_attn_abi_version(void);
 int32_t pth_attn_attn_args_bytes(void);
 int32_t pth_attn_combine_args_bytes(void);
 int32_t pth_attn_options_bytes(void);
+/* sizeof(PthAttnWriteArgs). No counterpart in the reference (see above). */
+int32_t pth_attn_write_args_bytes(void);
 /* 1: the library holds GPU kernels (always). Reference: attn_capi.h:86 */
 int32_t pth_attn_has_cuda(void);
 /* Message of the calling thread's last failure ("" after a success).
@@ -201,6 +235,13 @@ int32_t pth_attn_attention_lse(const PthAttnArgs* args, float* lse,
  * slots are not filled). With the combine of pth_attn_attention_lse this is
  * the op's layer call. No counterpart in the reference's ABI. */
 int32_t pth_attn_attention_kernel(const PthAttnArgs* args, void* stream);
+
+/* The int8 per-token-head cache writer: per (token, KV head), the fp32
+ * absmax scale max(absmax / 127, 1e-6) and int8 = trunc(clamp(x * (1 /
+ * scale) +- 0.5, -128, 127)), step for step as vLLM's writer (the reference's
+ * mirror: python/pth_testing/reference.py:76-103), into the cache cells.
+ * Enqueued on `stream`, no sync. No counterpart in the reference's ABI. */
+int32_t pth_attn_write_kv(const PthAttnWriteArgs* args, void* stream);
 
 #ifdef __cplusplus
 } /* extern "C" */

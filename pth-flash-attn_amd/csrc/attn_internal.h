@@ -136,6 +136,9 @@ int32_t rows_block_tokens(int32_t group);
 hipError_t launch_combine_kernel(const CombineParams& c, hipStream_t stream);
 hipError_t launch_fill_unused_splits(const CombineParams& c, hipStream_t stream);
 
+// The int8 cache writer (attn_writer.hip).
+int32_t launch_write_kv(const PthAttnWriteArgs& a, hipStream_t stream);
+
 const char* last_error();
 int32_t fail(int32_t code, const std::string& msg);
 void clear_error();

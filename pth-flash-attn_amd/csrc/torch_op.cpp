@@ -406,6 +406,76 @@ void pth_flash_attn_fwd(const Tensor& out, const Tensor& q, const Tensor& k_cach
                  window, causal);
 }
 
+#define PFW_CHECK(cond, ...) TORCH_CHECK((cond), "reshape_and_cache_int8: ", __VA_ARGS__)
+
+// vLLM's int8_per_token_head cache write (no op of the reference: it uses
+// vLLM's Triton writer, mirrored by python/pth_testing/reference.py:76-103):
+// key / value [T, Hkv, D] (fp32, fp16 or bf16) into the four cache views of
+// pth_flash_attn_fwd, token t at slot slot_mapping[t] (< 0: skipped).
+void reshape_and_cache_int8(const Tensor& key, const Tensor& value, const Tensor& k_cache,
+                            const Tensor& v_cache, const Tensor& k_scale,
+                            const Tensor& v_scale, const Tensor& slot_mapping) {
+  PFW_CHECK(key.dim() == 3 && value.dim() == 3, "key and value must be 3-D [T, Hkv, D]");
+  PFW_CHECK(key.sizes() == value.sizes(), "key and value must have the same shape");
+  PFW_CHECK(key.scalar_type() == value.scalar_type() &&
+                (key.scalar_type() == at::kFloat || key.scalar_type() == at::kHalf ||
+                 key.scalar_type() == at::kBFloat16),
+            "key and value must both be float32, float16 or bfloat16");
+  PFW_CHECK(key.stride(2) == 1 && value.stride(2) == 1,
+            "key and value must have stride 1 in their last dimension");
+  const int64_t T = key.size(0), Hkv = key.size(1), D = key.size(2);
+  PFW_CHECK(D == 64 || D == 128 || D == 256, "head size must be 64, 128 or 256, got ", D);
+  PFW_CHECK(k_cache.dim() == 4 && v_cache.dim() == 4 && k_cache.scalar_type() == at::kChar &&
+                v_cache.scalar_type() == at::kChar,
+            "k_cache and v_cache must be 4-D int8 [num_blocks, block_size, Hkv, D]");
+  PFW_CHECK(k_cache.sizes() == v_cache.sizes() && k_cache.size(2) == Hkv && k_cache.size(3) == D,
+            "k_cache and v_cache must be [num_blocks, block_size, ", Hkv, ", ", D, "]");
+  PFW_CHECK(k_cache.stride(3) == 1 && v_cache.stride(3) == 1,
+            "k_cache and v_cache must have stride 1 in their last dimension");
+  PFW_CHECK(k_scale.dim() == 3 && v_scale.dim() == 3 && k_scale.scalar_type() == at::kFloat &&
+                v_scale.scalar_type() == at::kFloat &&
+                k_scale.sizes() == k_cache.sizes().slice(0, 3) &&
+                v_scale.sizes() == k_cache.sizes().slice(0, 3),
+            "k_scale and v_scale must be float32 [num_blocks, block_size, Hkv]");
+  PFW_CHECK(slot_mapping.dim() == 1 && slot_mapping.size(0) == T &&
+                slot_mapping.scalar_type() == at::kLong,
+            "slot_mapping must be int64 [T]");
+  const Tensor* all[] = {&value, &k_cache, &v_cache, &k_scale, &v_scale, &slot_mapping};
+  for (const Tensor* t : all)
+    PFW_CHECK(t->device() == key.device(), "all tensors must be on the device of key");
+  PFW_CHECK(key.is_cuda(),
+            "arguments are valid, but the op computes on CUDA tensors only (the CPU "
+            "registration exists to test the argument checks)");
+  if (T == 0) return;
+  const c10::hip::HIPGuardMasqueradingAsCUDA guard(key.device());
+  PthAttnWriteArgs a{};
+  a.abi_version = PTH_ATTN_ABI_VERSION;
+  a.struct_bytes = static_cast<int32_t>(sizeof(PthAttnWriteArgs));
+  a.key = key.data_ptr();
+  a.value = value.data_ptr();
+  a.key_stride_token = byte_stride(key, 0);
+  a.key_stride_head = byte_stride(key, 1);
+  a.value_stride_token = byte_stride(value, 0);
+  a.value_stride_head = byte_stride(value, 1);
+  a.kv_dtype = key.scalar_type() == at::kFloat ? PTH_ATTN_F32
+               : key.scalar_type() == at::kHalf ? PTH_ATTN_F16
+                                                : PTH_ATTN_BF16;
+  a.num_tokens = static_cast<int32_t>(T);
+  a.num_kv_heads = static_cast<int32_t>(Hkv);
+  a.head_size = static_cast<int32_t>(D);
+  a.slot_mapping = slot_mapping.data_ptr<int64_t>();
+  a.k_cache = stream_of(k_cache);
+  a.v_cache = stream_of(v_cache);
+  a.k_scale = stream_of(k_scale);
+  a.v_scale = stream_of(v_scale);
+  a.block_size = static_cast<int32_t>(k_cache.size(1));
+  a.num_blocks = static_cast<int32_t>(k_cache.size(0));
+  const hipStream_t stream =
+      c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(key.get_device()).stream();
+  const int32_t rc = pa::launch_write_kv(a, stream);
+  PFW_CHECK(rc == PTH_ATTN_OK, pa::last_error());
+}
+
 }  // namespace
 
 // Schema text identical to the reference's (torch_bindings.cpp:20-27,
@@ -417,9 +487,19 @@ TORCH_LIBRARY(pth_flash_attn, m) {
       "Tensor seq_lens, Tensor query_start_loc, int max_query_len, int wm, "
       "int num_splits, float softmax_scale, Tensor! ws_o, Tensor! ws_lse, "
       "int window=0, bool causal=True) -> ()");
+  // The cache writer (no counterpart in the reference; see above).
+  m.def(
+      "reshape_and_cache_int8(Tensor key, Tensor value, Tensor! k_cache, Tensor! v_cache, "
+      "Tensor! k_scale, Tensor! v_scale, Tensor slot_mapping) -> ()");
 }
 
-TORCH_LIBRARY_IMPL(pth_flash_attn, CUDA, m) { m.impl("pth_flash_attn_fwd", &pth_flash_attn_fwd); }
+TORCH_LIBRARY_IMPL(pth_flash_attn, CUDA, m) {
+  m.impl("pth_flash_attn_fwd", &pth_flash_attn_fwd);
+  m.impl("reshape_and_cache_int8", &reshape_and_cache_int8);
+}
 
 // Validates, then raises: CPU tensors exist only to test the checks.
-TORCH_LIBRARY_IMPL(pth_flash_attn, CPU, m) { m.impl("pth_flash_attn_fwd", &pth_flash_attn_fwd); }
+TORCH_LIBRARY_IMPL(pth_flash_attn, CPU, m) {
+  m.impl("pth_flash_attn_fwd", &pth_flash_attn_fwd);
+  m.impl("reshape_and_cache_int8", &reshape_and_cache_int8);
+}

@@ -35,6 +35,8 @@ EXPORTED_SYMBOLS = (
     "pth_attn_combine",
     "pth_attn_attention_lse",
     "pth_attn_attention_kernel",
+    "pth_attn_write_args_bytes",
+    "pth_attn_write_kv",
 )
 
 
@@ -116,6 +118,30 @@ class PthAttnCombineArgs(ctypes.Structure):
     ]
 
 
+class PthAttnWriteArgs(ctypes.Structure):
+    _fields_ = [
+        ("abi_version", ctypes.c_int32),
+        ("struct_bytes", ctypes.c_int32),
+        ("key", ctypes.c_void_p),
+        ("value", ctypes.c_void_p),
+        ("key_stride_token", ctypes.c_int64),
+        ("key_stride_head", ctypes.c_int64),
+        ("value_stride_token", ctypes.c_int64),
+        ("value_stride_head", ctypes.c_int64),
+        ("kv_dtype", ctypes.c_int32),
+        ("num_tokens", ctypes.c_int32),
+        ("num_kv_heads", ctypes.c_int32),
+        ("head_size", ctypes.c_int32),
+        ("slot_mapping", ctypes.c_void_p),
+        ("k_cache", PthAttnStream),
+        ("v_cache", PthAttnStream),
+        ("k_scale", PthAttnStream),
+        ("v_scale", PthAttnStream),
+        ("block_size", ctypes.c_int32),
+        ("num_blocks", ctypes.c_int32),
+    ]
+
+
 class PthAttnOptions(ctypes.Structure):
     _fields_ = [
         ("abi_version", ctypes.c_int32),
@@ -142,6 +168,7 @@ class AttnLib:
             "pth_attn_combine_args_bytes",
             "pth_attn_options_bytes",
             "pth_attn_has_cuda",
+            "pth_attn_write_args_bytes",
         ):
             getattr(lib, name).restype = i32
             getattr(lib, name).argtypes = []
@@ -162,7 +189,13 @@ class AttnLib:
         lib.pth_attn_attention_lse.restype = i32
         lib.pth_attn_attention_lse.argtypes = [
             ctypes.POINTER(PthAttnArgs), vp, ctypes.c_int64, ctypes.c_int64, vp]
+        lib.pth_attn_write_kv.restype = i32
+        lib.pth_attn_write_kv.argtypes = [ctypes.POINTER(PthAttnWriteArgs), vp]
         self.lib = lib
+
+    def write_kv(self, args: PthAttnWriteArgs, stream: int | None = None) -> int:
+        """The int8 cache writer (see include/pth_attn.h)."""
+        return self.lib.pth_attn_write_kv(ctypes.byref(args), stream)
 
     def last_error(self) -> str:
         return self.lib.pth_attn_last_error().decode()
@@ -288,3 +321,23 @@ def combine_args(*, ws_o: Any, ws_lse: Any, out: Any, query_start_loc: Any,
     c.head_size = int(out.shape[2])
     c.num_splits = num_splits
     return c
+
+
+def write_args(*, key: Any, value: Any, k_cache: Any, v_cache: Any, k_scale: Any, v_scale: Any,
+               slot_mapping: Any) -> PthAttnWriteArgs:
+    """PthAttnWriteArgs of torch tensors (raw pointers: keep the tensors alive)."""
+    a = PthAttnWriteArgs()
+    a.abi_version = ABI_VERSION
+    a.struct_bytes = ctypes.sizeof(PthAttnWriteArgs)
+    a.key, a.value = key.data_ptr(), value.data_ptr()
+    a.key_stride_token, a.key_stride_head = _bstride(key, 0), _bstride(key, 1)
+    a.value_stride_token, a.value_stride_head = _bstride(value, 0), _bstride(value, 1)
+    import torch
+    a.kv_dtype = {torch.float32: PTH_ATTN_F32, torch.float16: PTH_ATTN_F16,
+                  torch.bfloat16: PTH_ATTN_BF16}[key.dtype]
+    a.num_tokens, a.num_kv_heads, a.head_size = (int(x) for x in key.shape)
+    a.slot_mapping = slot_mapping.data_ptr()
+    a.k_cache, a.v_cache = _stream(k_cache), _stream(v_cache)
+    a.k_scale, a.v_scale = _stream(k_scale), _stream(v_scale)
+    a.num_blocks, a.block_size = int(k_cache.shape[0]), int(k_cache.shape[1])
+    return a

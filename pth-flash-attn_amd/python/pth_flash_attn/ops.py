@@ -250,11 +250,33 @@ def pth_flash_attn_fwd_fake(
     )
 
 
+# The int8 cache writer registered by the same library (no counterpart in the
+# reference, which relies on vLLM's Triton writer; see include/pth_attn.h).
+WRITER_NAME = "reshape_and_cache_int8"
+WRITER_QUALNAME = f"{OP_NAMESPACE}::{WRITER_NAME}"
+WRITER_SCHEMA = (
+    "reshape_and_cache_int8(Tensor key, Tensor value, Tensor! k_cache, Tensor! v_cache, "
+    "Tensor! k_scale, Tensor! v_scale, Tensor slot_mapping) -> ()"
+)
+
+
+def reshape_and_cache_int8_fake(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor,
+                                v_cache: torch.Tensor, k_scale: torch.Tensor,
+                                v_scale: torch.Tensor, slot_mapping: torch.Tensor) -> None:
+    """Fake of the writer (an in-place op: nothing to create)."""
+    if key.dim() != 3 or key.shape != value.shape:
+        raise RuntimeError("reshape_and_cache_int8: key and value must be 3-D [T, Hkv, D] "
+                           "of the same shape")
+    if slot_mapping.dim() != 1 or slot_mapping.shape[0] != key.shape[0]:
+        raise RuntimeError("reshape_and_cache_int8: slot_mapping must be int64 [T]")
+
+
 def _load_library() -> bool:
     if not LIBRARY_PATH.is_file():
         return False
     torch.ops.load_library(str(LIBRARY_PATH))
     torch.library.register_fake(OP_QUALNAME)(pth_flash_attn_fwd_fake)
+    torch.library.register_fake(WRITER_QUALNAME)(reshape_and_cache_int8_fake)
     return True
 
 
@@ -309,3 +331,24 @@ def pth_flash_attn_fwd(
         query_start_loc, max_query_len, wm, num_splits, softmax_scale, ws_o,
         ws_lse, window, causal,
     )
+
+
+def reshape_and_cache_int8(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor,
+                           v_cache: torch.Tensor, k_scale: torch.Tensor, v_scale: torch.Tensor,
+                           slot_mapping: torch.Tensor) -> None:
+    """Quantise ``key`` / ``value`` [T, Hkv, D] into the int8_per_token_head cache.
+
+    Token t goes to slot ``slot_mapping[t]`` (page ``slot // block_size``,
+    in-page slot ``slot % block_size``; a negative slot skips the token). Per
+    (token, head): scale = max(absmax / 127, 1e-6) in fp32 and
+    int8 = trunc(clamp(x * (1 / scale) +- 0.5, -128, 127)), as vLLM's writer
+    (mirrored by the reference's python/pth_testing/reference.py:76-103).
+    The caches are the four views ``pth_flash_attn_fwd`` reads.
+    """
+    if not _LIBRARY_LOADED:
+        raise RuntimeError(
+            f"reshape_and_cache_int8: op library {LIBRARY_PATH} is not built; run "
+            "python pth-flash-attn_amd/build.py"
+        )
+    torch.ops.pth_flash_attn.reshape_and_cache_int8.default(
+        key, value, k_cache, v_cache, k_scale, v_scale, slot_mapping)

@@ -59,11 +59,13 @@ def test_identity_and_struct_sizes(lib):
     assert L.pth_attn_attn_args_bytes() == ctypes.sizeof(capi.PthAttnArgs) == 352
     assert L.pth_attn_combine_args_bytes() == ctypes.sizeof(capi.PthAttnCombineArgs) == 136
     assert L.pth_attn_options_bytes() == ctypes.sizeof(capi.PthAttnOptions) == 12
+    assert L.pth_attn_write_args_bytes() == ctypes.sizeof(capi.PthAttnWriteArgs)
     assert L.pth_attn_has_cuda() == 1
 
 
 @pytest.mark.skipif(shutil.which("gcc") is None, reason="needs gcc")
-@pytest.mark.parametrize("struct", [capi.PthAttnArgs, capi.PthAttnCombineArgs, capi.PthAttnOptions])
+@pytest.mark.parametrize("struct", [capi.PthAttnArgs, capi.PthAttnCombineArgs, capi.PthAttnOptions,
+                                    capi.PthAttnWriteArgs])
 def test_ctypes_mirror_matches_the_header(struct, tmp_path):
     """Every field offset of the ctypes mirror equals offsetof() in the C header."""
     name = struct.__name__
@@ -194,3 +196,25 @@ def test_error_is_cleared_by_a_success(lib):
     assert lib.attention(a) == capi.PTH_ATTN_EINVAL
     lib.tiling(128, 4, 4)
     assert lib.last_error() == ""
+
+
+@needs_lib
+def test_writer_rejects_invalid_arguments(lib):
+    key = torch.zeros(2, 2, 128, dtype=torch.bfloat16)
+    cell = torch.zeros(3, 16, 2, 264, dtype=torch.int8)
+    sm = torch.zeros(2, dtype=torch.int64)
+    w = capi.write_args(key=key, value=key, k_cache=cell[..., :128], v_cache=cell[..., 132:260],
+                        k_scale=cell[..., 128:132].view(torch.float32)[..., 0],
+                        v_scale=cell[..., 260:].view(torch.float32)[..., 0], slot_mapping=sm)
+    w.head_size = 96
+    assert lib.write_kv(w) == capi.PTH_ATTN_EINVAL
+    assert "head_size" in lib.last_error()
+    w.head_size = 128
+    w.kv_dtype = 7
+    assert lib.write_kv(w) == capi.PTH_ATTN_EINVAL
+    assert "kv_dtype" in lib.last_error()
+    w.kv_dtype = capi.PTH_ATTN_BF16
+    w.struct_bytes = 8
+    assert lib.write_kv(w) == capi.PTH_ATTN_EINVAL
+    assert "sizeof(PthAttnWriteArgs)" in lib.last_error()
+    assert lib.lib.pth_attn_write_kv(None, None) == capi.PTH_ATTN_EINVAL
