@@ -18,9 +18,10 @@
 // Lane l owns columns [l NC, (l + 1) NC), NC = D / 64, so a split's row is
 // one coalesced 4 D-byte read. Lane s loads lse_s (64 splits per instruction);
 // the weights are broadcast with readlane and the o loads of 16 splits are
-// issued before their fused multiply-adds. When the launcher
-// passes the request lengths, only the splits the attention kernel wrote for
-// the row are read (attn_stream.h), and a row with a single split is left as
+// issued before their fused multiply-adds. On the op path (the launcher
+// passes the request lengths) only the splits the attention kernel wrote for
+// the row are read: their count is the marker the kernel left in the row's
+// last LSE slot (attn_device.h), and a row with a single split is left as
 // the attention kernel wrote it to out.
 
 #include "attn_stream.h"
@@ -36,7 +37,9 @@ typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 
 constexpr float kNegInf = -__builtin_inff();
-constexpr int kBatch = 16;
+// Splits whose o loads are issued together (before their multiply-adds).
+template <int NC>
+constexpr int kBatch = 32 / NC;
 
 __device__ __forceinline__ float wave_max(float x) {
 #pragma unroll
@@ -92,6 +95,24 @@ __device__ __forceinline__ int row_live_splits(const CombineParams& c, int r, in
   return live;
 }
 
+// Splits of row (tok, head) on the op path: the count the attention kernel
+// recorded in the row's last log2-LSE slot (a quiet NaN with the count as
+// payload, attn_device.h), or all num_splits when the slot holds a real LSE.
+__device__ __forceinline__ int marked_splits(const CombineParams& c, int64_t tok, int head) {
+  const uint32_t bits = *reinterpret_cast<const uint32_t*>(
+      c.ws_lse + static_cast<int64_t>(c.num_splits - 1) * c.s_wl_split + tok * c.s_wl_tok +
+      static_cast<int64_t>(head) * c.s_wl_head);
+  const uint32_t n = bits & 0x003fffffu;
+  return (bits & 0xffc00000u) == 0x7fc00000u && n >= 1 && n < static_cast<uint32_t>(c.num_splits)
+             ? static_cast<int>(n)
+             : c.num_splits;
+}
+
+// Padding rows (tokens at or beyond qsl[R]) are never read or written.
+__device__ __forceinline__ bool padding_token(const CombineParams& c, int64_t tok) {
+  return tok >= ld_ro(c.qsl, c.num_reqs);
+}
+
 // NC consecutive fp32 columns at p (4 NC-byte aligned).
 template <int NC>
 __device__ __forceinline__ void load_cols(const char* p, float (&x)[NC]) {
@@ -109,17 +130,20 @@ __device__ __forceinline__ void load_cols(const char* p, float (&x)[NC]) {
 // Merges splits of the 64-split blocks first, first + step, ... of row
 // (tok, head): the maximum M of their log2-LSEs and, relative to it, this
 // lane's NC numerator columns and the (wave-summed) denominator.
-template <int NC>
+template <int NC, int kBlk = 64>
 __device__ __forceinline__ void merge_blocks(const CombineParams& c, int64_t tok, int head, int S,
                                              int first, int step, int lane, float& M,
                                              float (&num)[NC], float& den) {
+  constexpr int kB = kBatch<NC> < kBlk ? kBatch<NC> : kBlk;
   const char* lse_row = c.ws_lse + tok * c.s_wl_tok + static_cast<int64_t>(head) * c.s_wl_head;
   const char* o_row =
       c.ws_o + tok * c.s_wo_tok + static_cast<int64_t>(head) * c.s_wo_head + 4 * NC * lane;
   M = kNegInf;
-  for (int s = 64 * first + lane; s < S; s += 64 * step) {
-    const float x = *reinterpret_cast<const float*>(lse_row + s * c.s_wl_split);
-    M = x > M ? x : M;  // -inf and NaN never win
+  if (lane < kBlk) {
+    for (int s = kBlk * first + lane; s < S; s += kBlk * step) {
+      const float x = *reinterpret_cast<const float*>(lse_row + s * c.s_wl_split);
+      M = x > M ? x : M;  // -inf and NaN never win
+    }
   }
   M = wave_max(M);
 #pragma unroll
@@ -127,17 +151,18 @@ __device__ __forceinline__ void merge_blocks(const CombineParams& c, int64_t tok
   den = 0.0f;
   if (!(M > kNegInf)) return;
   float den_l = 0.0f;
-  for (int s0 = 64 * first; s0 < S; s0 += 64 * step) {
+  for (int s0 = kBlk * first; s0 < S; s0 += kBlk * step) {
     const int s = s0 + lane;
-    const float x = s < S ? *reinterpret_cast<const float*>(lse_row + s * c.s_wl_split) : kNegInf;
+    const float x = lane < kBlk && s < S ? *reinterpret_cast<const float*>(lse_row + s * c.s_wl_split)
+                                         : kNegInf;
     const float w_l = x > kNegInf ? __builtin_amdgcn_exp2f(x - M) : 0.0f;
     den_l += w_l;
-    const int n = S - s0 < 64 ? S - s0 : 64;
-    for (int e0 = 0; e0 < n; e0 += kBatch) {
-      float w[kBatch];
-      float ov[kBatch][NC];
+    const int n = S - s0 < kBlk ? S - s0 : kBlk;
+    for (int e0 = 0; e0 < n; e0 += kB) {
+      float w[kB];
+      float ov[kB][NC];
 #pragma unroll
-      for (int k = 0; k < kBatch; ++k) {
+      for (int k = 0; k < kB; ++k) {
         const int e = e0 + k;
         w[k] = e < n ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(
                                                       __builtin_bit_cast(int, w_l), e))
@@ -150,7 +175,7 @@ __device__ __forceinline__ void merge_blocks(const CombineParams& c, int64_t tok
         }
       }
 #pragma unroll
-      for (int k = 0; k < kBatch; ++k) {
+      for (int k = 0; k < kB; ++k) {
         if (w[k] > 0.0f) {
 #pragma unroll
           for (int i = 0; i < NC; ++i) num[i] = fmaf(w[k], ov[k][i], num[i]);
@@ -206,58 +231,48 @@ __device__ __forceinline__ void write_row(const CombineParams& c, int64_t tok, i
   }
 }
 
-// Rows with more splits than this are merged by all 4 waves of the
-// work-group together; the others by wave 0 alone.
-constexpr int kSharedRowSplits = 64;
-
+// One wave per (token, head) row, whatever its split count.
 template <int D>
 __global__ __launch_bounds__(256) void combine_splits(const CombineParams c) {
   constexpr int NC = D / 64;  // columns per lane
-  __shared__ int row_splits;
-  __shared__ float part_m[kWaves], part_den[kWaves];
-  __shared__ float part_num[kWaves][NC][64];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  if (!c.shared_rows) {  // one row per wave, whatever its split count
-    const int64_t row = static_cast<int64_t>(blockIdx.x) * kWaves + wave;
-    const int64_t tok = row / c.num_q_heads;
-    const int head = static_cast<int>(row - tok * c.num_q_heads);
-    if (tok >= c.num_tokens) return;
-    const int r = request_of_token(c, tok, lane);
-    if (r >= c.num_reqs) return;  // a padding row beyond qsl[R]
-    const int S = c.seq_lens != nullptr ? row_live_splits(c, r, tok, head, lane) : c.num_splits;
-    if (c.seq_lens != nullptr && S == 1) return;  // written to out by the attention kernel
-    float M, den;
-    float num[NC];
-    merge_blocks<NC>(c, tok, head, S, 0, 1, lane, M, num, den);
-    write_row<NC>(c, tok, head, M, num, den, lane);
-    return;
-  }
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * kWaves + wave;
+  const int64_t tok = row / c.num_q_heads;
+  const int head = static_cast<int>(row - tok * c.num_q_heads);
+  if (tok >= c.num_tokens) return;
+  // Both loads in flight together.
+  const int S = c.seq_lens != nullptr ? marked_splits(c, tok, head) : c.num_splits;
+  if (padding_token(c, tok)) return;
+  if (c.seq_lens != nullptr && S == 1) return;  // written to out by the attention kernel
+  float M, den;
+  float num[NC];
+  merge_blocks<NC>(c, tok, head, S, 0, 1, lane, M, num, den);
+  write_row<NC>(c, tok, head, M, num, den, lane);
+}
+
+// Few rows with many splits (shared_rows): a work-group of 16 waves per row;
+// wave w merges the 16-split blocks w, w + 16, ... (one round of loads for
+// up to 256 splits) and wave 0 merges the 16 results in a fixed order.
+constexpr int kSharedWaves = 16;
+constexpr int kSharedBlock = 16;
+
+template <int D>
+__global__ __launch_bounds__(kSharedWaves * 64) void combine_shared(const CombineParams c) {
+  constexpr int NC = D / 64;
+  __shared__ float part_m[kSharedWaves], part_den[kSharedWaves];
+  __shared__ float part_num[kSharedWaves][NC][64];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int64_t row = blockIdx.x;
   const int64_t tok = row / c.num_q_heads;
   const int head = static_cast<int>(row - tok * c.num_q_heads);
-  if (wave == 0) {  // the row's split count (0: nothing to merge)
-    int S = 0;
-    const int r = request_of_token(c, tok, lane);
-    if (r < c.num_reqs) {  // not a padding row beyond qsl[R]
-      S = c.seq_lens != nullptr ? row_live_splits(c, r, tok, head, lane) : c.num_splits;
-      if (c.seq_lens != nullptr && S == 1) S = 0;  // written to out by the attention kernel
-    }
-    if (lane == 0) row_splits = S;
-  }
-  __syncthreads();
-  const int S = row_splits;
+  if (tok >= c.num_tokens || padding_token(c, tok)) return;  // uniform over the work-group
+  const int S = c.seq_lens != nullptr ? marked_splits(c, tok, head) : c.num_splits;
+  if (c.seq_lens != nullptr && S == 1) return;  // written to out by the attention kernel
   float M, den;
   float num[NC];
-  if (S <= kSharedRowSplits) {
-    if (wave != 0 || S == 0) return;
-    merge_blocks<NC>(c, tok, head, S, 0, 1, lane, M, num, den);
-    write_row<NC>(c, tok, head, M, num, den, lane);
-    return;
-  }
-  // The 4 waves take the 64-split blocks in turn; wave 0 merges their
-  // results in a fixed order.
-  merge_blocks<NC>(c, tok, head, S, wave, kWaves, lane, M, num, den);
+  merge_blocks<NC, kSharedBlock>(c, tok, head, S, wave, kSharedWaves, lane, M, num, den);
   if (lane == 0) {
     part_m[wave] = M;
     part_den[wave] = den;
@@ -268,14 +283,14 @@ __global__ __launch_bounds__(256) void combine_splits(const CombineParams c) {
   if (wave != 0) return;
   float Mg = kNegInf;
 #pragma unroll
-  for (int w = 0; w < kWaves; ++w) Mg = part_m[w] > Mg ? part_m[w] : Mg;
+  for (int w = 0; w < kSharedWaves; ++w) Mg = part_m[w] > Mg ? part_m[w] : Mg;
   float ng[NC];
 #pragma unroll
   for (int i = 0; i < NC; ++i) ng[i] = 0.0f;
   float dg = 0.0f;
   if (Mg > kNegInf) {
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
+    for (int w = 0; w < kSharedWaves; ++w) {
       if (part_m[w] > kNegInf) {
         const float a = __builtin_amdgcn_exp2f(part_m[w] - Mg);
 #pragma unroll
@@ -307,6 +322,16 @@ __global__ __launch_bounds__(256) void fill_unused_splits(const CombineParams c)
     *reinterpret_cast<float*>(lse_row + s * c.s_wl_split) = kNegInf;
 }
 
+template <int D>
+void launch_combine_d(const CombineParams& c, int64_t rows, hipStream_t stream) {
+  if (c.shared_rows)
+    hipLaunchKernelGGL(combine_shared<D>, dim3(static_cast<unsigned>(rows)),
+                       dim3(kSharedWaves * 64), 0, stream, c);
+  else
+    hipLaunchKernelGGL(combine_splits<D>, dim3(static_cast<unsigned>((rows + kWaves - 1) / kWaves)),
+                       dim3(kWaves * 64), 0, stream, c);
+}
+
 }  // namespace
 
 hipError_t launch_fill_unused_splits(const CombineParams& c, hipStream_t stream) {
@@ -318,16 +343,10 @@ hipError_t launch_fill_unused_splits(const CombineParams& c, hipStream_t stream)
 
 hipError_t launch_combine_kernel(const CombineParams& c, hipStream_t stream) {
   const int64_t rows = static_cast<int64_t>(c.num_tokens) * c.num_q_heads;
-  const unsigned blocks = static_cast<unsigned>(c.shared_rows ? rows : (rows + kWaves - 1) / kWaves);
   switch (c.head_size) {
-    case 64:
-      hipLaunchKernelGGL(combine_splits<64>, dim3(blocks), dim3(kWaves * 64), 0, stream, c);
-      break;
-    case 256:
-      hipLaunchKernelGGL(combine_splits<256>, dim3(blocks), dim3(kWaves * 64), 0, stream, c);
-      break;
-    default:
-      hipLaunchKernelGGL(combine_splits<128>, dim3(blocks), dim3(kWaves * 64), 0, stream, c);
+    case 64: launch_combine_d<64>(c, rows, stream); break;
+    case 256: launch_combine_d<256>(c, rows, stream); break;
+    default: launch_combine_d<128>(c, rows, stream);
   }
   return hipGetLastError();
 }

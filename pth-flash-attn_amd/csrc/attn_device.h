@@ -587,15 +587,29 @@ __device__ __forceinline__ bool direct_out(const AttnParams& p, int live) {
   return p.num_splits == 1 || (live == 1 && p.direct_single != 0);
 }
 
+// Split count marker. On the op path (direct_single) the combine must know
+// how many splits a row has. The unit that computes split 0 of a row with
+// live < num_splits splits records live in the row's last log2-LSE slot,
+// num_splits - 1, which no split of the row uses: as a quiet NaN whose
+// payload is live (a real LSE is finite or -inf, and a NaN produced by
+// arithmetic has payload 0). With live == num_splits no marker is written
+// and the combine reads all splits.
+constexpr uint32_t kSplitMarker = 0x7fc00000u;
+__device__ __forceinline__ bool writes_marker(const AttnParams& p, int s, int live) {
+  return p.direct_single != 0 && p.num_splits > 1 && s == 0 && live < p.num_splits;
+}
+
 // Vector memory instructions store_finished issues for a unit, known before
 // it is issued (the lanes without a row are masked off, never the whole
 // wave: row 0 of a unit always exists), so that the waits of the chunk
 // pipeline can count past them.
 template <int D = 128>
-__device__ __forceinline__ int stores_per_unit(const AttnParams& p, int live) {
+__device__ __forceinline__ int stores_per_unit(const AttnParams& p, int s, int live) {
   constexpr int kCols = HeadDim<D>::kCols;
-  if (!direct_out(p, live)) return kCols / 4 + 1;
-  return (p.out_dtype == PTH_ATTN_F32 ? kCols / 4 : kCols / 8) + (p.lse_out != nullptr ? 1 : 0);
+  const int marker = writes_marker(p, s, live) ? 1 : 0;
+  if (!direct_out(p, live)) return kCols / 4 + 1 + marker;
+  return (p.out_dtype == PTH_ATTN_F32 ? kCols / 4 : kCols / 8) + (p.lse_out != nullptr ? 1 : 0) +
+         marker;
 }
 
 // Stores a finished unit: out (and lse_out, natural log) or its split's
@@ -607,6 +621,11 @@ __device__ __forceinline__ void store_finished(const AttnParams& p, const Finish
   if (!f.vrow) return;
   const int g = f.g;
   const int64_t head = f.head;
+  if (writes_marker(p, f.s, f.live)) {
+    char* lse_row = reinterpret_cast<char*>(p.ws_lse) + f.qtok * p.s_wl_tok + head * p.s_wl_head;
+    *reinterpret_cast<uint32_t*>(lse_row + static_cast<int64_t>(p.num_splits - 1) * p.s_wl_split) =
+        kSplitMarker | static_cast<uint32_t>(f.live);
+  }
   if (!direct_out(p, f.live)) {
     char* dst = reinterpret_cast<char*>(p.ws_o) + f.s * p.s_wo_split + f.qtok * p.s_wo_tok +
                 head * p.s_wo_head + 4 * kCols * g;

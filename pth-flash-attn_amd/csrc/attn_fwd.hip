@@ -222,7 +222,7 @@ void attn_fwd_paged(const AttnParams p) {
       __builtin_amdgcn_s_waitcnt(0x0F70);
       if (had) {
         store_finished(p, done);
-        n_store = stores_per_unit(p, done.live);
+        n_store = stores_per_unit(p, done.s, done.live);
         older_than_stores = inflight;
       }
       if (!have) break;
