@@ -1,0 +1,129 @@
+// read_ceiling.hip -- achievable HBM read bandwidth on one MI355X for the paged
+// cell layout of the attention kernels (8 KV heads x 264-byte cells, pages of
+// 16 tokens, a shuffled page order over ~2.2 GB). Each variant reads every
+// byte of every page once and discards it:
+//   * head: per-head cells as the attention kernels read them (register
+//     loads of K, V and the scales of one head per wave, U 16-token groups
+//     in flight);
+//   * rows: whole pages (33 contiguous KB) per wave, P loads in flight;
+//   * rows pipe: whole pages, the next page's 33 loads issued before the
+//     current one is consumed.
+// Not part of the library: a measurement of the ceiling that the kernels'
+// roofline fractions are read against.
+//
+// Build and run (from the repository root, on the GPU):
+//   hipcc -O3 --offload-arch=gfx950 -Xclang -target-feature -Xclang -packed-fp32-ops \
+//     pth-flash-attn_amd/probes/read_ceiling.hip -o /tmp/read_ceiling && /tmp/read_ceiling
+#include <hip/hip_runtime.h>
+#include <cstdio>
+#include <cstdlib>
+#include <vector>
+#include <algorithm>
+#include <random>
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4a __attribute__((ext_vector_type(4), aligned(4)));
+#define CK(x) do{hipError_t e=(x); if(e!=hipSuccess){printf("err %s line %d\n",hipGetErrorString(e),__LINE__);exit(1);}}while(0)
+constexpr int PAGE = 16 * 8 * 264;  // 33792 = 33 KB
+
+// per-head cell reads (the current kernel's pattern), register loads, U groups in flight
+template <int U>
+__global__ __launch_bounds__(512) void rd_head(const char* base, const int* pages, int npages, int per_wg, uint32_t* out) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int pb = blockIdx.x * per_wg, pe = min(npages, pb + per_wg);
+  uint32_t acc = 0;
+  const int tok = lane >> 3, piece = lane & 7;
+  for (int pg = pb; pg < pe; pg += U) {
+    u32x4 k[U][2], v[U][2];
+    uint32_t s[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int pgi = min(pg + u, pe - 1);
+      const char* page = base + (size_t)pages[pgi] * PAGE;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const char* cell = page + (size_t)(8 * h + tok) * 2112 + wave * 264;
+        k[u][h] = *(const u32x4a*)(cell + 16 * piece);
+        v[u][h] = *(const u32x4a*)(cell + 132 + 16 * piece);
+      }
+      s[u] = *(const uint32_t*)(page + (size_t)(lane & 15) * 2112 + wave * 264 + (lane < 16 ? 128 : 260));
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) acc ^= k[u][0].x ^ k[u][1].y ^ v[u][0].z ^ v[u][1].w ^ s[u];
+  }
+  if (acc == 0x12345678) out[0] = acc;
+}
+
+// whole-page (token-row) reads: wave w of the work-group reads pages pb + w, + 8, ...;
+// a page is 33 contiguous KB: 33 loads of 16 B per lane. P loads per batch in flight.
+template <int P>
+__global__ __launch_bounds__(512) void rd_rows(const char* base, const int* pages, int npages, int per_wg, uint32_t* out) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int pb = blockIdx.x * per_wg, pe = min(npages, pb + per_wg);
+  uint32_t acc = 0;
+  for (int pg = pb + wave; pg < pe; pg += 8) {
+    const char* page = base + (size_t)pages[pg] * PAGE + 16 * lane;
+    for (int i0 = 0; i0 < 33; i0 += P) {
+      u32x4 x[P];
+#pragma unroll
+      for (int i = 0; i < P; ++i) x[i] = i0 + i < 33 ? *(const u32x4a*)(page + 1024 * (i0 + i)) : (u32x4){0,0,0,0};
+#pragma unroll
+      for (int i = 0; i < P; ++i) acc ^= x[i].x ^ x[i].w;
+    }
+  }
+  if (acc == 0x12345678) out[0] = acc;
+}
+
+// whole pages, all 33 loads of a page in flight, next page's loads issued before consuming
+__global__ __launch_bounds__(512) void rd_rows_pipe(const char* base, const int* pages, int npages, int per_wg, uint32_t* out) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int pb = blockIdx.x * per_wg, pe = min(npages, pb + per_wg);
+  uint32_t acc = 0;
+  u32x4 a[33];
+  int pg = pb + wave;
+  if (pg < pe) {
+    const char* page = base + (size_t)pages[pg] * PAGE + 16 * lane;
+#pragma unroll
+    for (int i = 0; i < 33; ++i) a[i] = *(const u32x4a*)(page + 1024 * i);
+  }
+  for (; pg < pe; pg += 8) {
+#pragma unroll
+    for (int i = 0; i < 33; ++i) acc ^= a[i].x ^ a[i].w;
+    const int nx = pg + 8;
+    if (nx < pe) {
+      const char* page = base + (size_t)pages[nx] * PAGE + 16 * lane;
+#pragma unroll
+      for (int i = 0; i < 33; ++i) a[i] = *(const u32x4a*)(page + 1024 * i);
+    }
+  }
+  if (acc == 0x12345678) out[0] = acc;
+}
+
+int main() {
+  const int npages = 66000;  // ~2.23 GB
+  size_t bytes = (size_t)npages * PAGE;
+  char* buf; uint32_t* out; int* pages;
+  CK(hipMalloc(&buf, bytes)); CK(hipMalloc(&out, 64)); CK(hipMalloc(&pages, npages * 4));
+  CK(hipMemset(buf, 1, bytes));
+  std::vector<int> perm(npages); for (int i = 0; i < npages; ++i) perm[i] = i;
+  std::mt19937 rng(1); std::shuffle(perm.begin(), perm.end(), rng);
+  CK(hipMemcpy(pages, perm.data(), npages * 4, hipMemcpyHostToDevice));
+  hipEvent_t a, b; CK(hipEventCreate(&a)); CK(hipEventCreate(&b));
+  int cus = 0; CK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, 0));
+  auto timeit = [&](const char* name, auto launch) {
+    launch(); CK(hipDeviceSynchronize());
+    CK(hipEventRecord(a));
+    for (int i = 0; i < 10; ++i) launch();
+    CK(hipEventRecord(b)); CK(hipEventSynchronize(b));
+    float ms; CK(hipEventElapsedTime(&ms, a, b));
+    printf("%-40s %8.1f us  %7.0f GB/s\n", name, ms * 100, bytes / (ms * 1e-4) / 1e9);
+  };
+  int grid = cus; int per = (npages + grid - 1) / grid;
+  timeit("head reg U=1", [&]{ rd_head<1><<<grid,512>>>(buf, pages, npages, per, out); });
+  timeit("head reg U=2", [&]{ rd_head<2><<<grid,512>>>(buf, pages, npages, per, out); });
+  timeit("rows P=4", [&]{ rd_rows<4><<<grid,512>>>(buf, pages, npages, per, out); });
+  timeit("rows P=11", [&]{ rd_rows<11><<<grid,512>>>(buf, pages, npages, per, out); });
+  timeit("rows P=33", [&]{ rd_rows<33><<<grid,512>>>(buf, pages, npages, per, out); });
+  timeit("rows pipe 2x33", [&]{ rd_rows_pipe<<<grid,512>>>(buf, pages, npages, per, out); });
+  timeit("rows P=11 grid x2", [&]{ rd_rows<11><<<2*grid,512>>>(buf, pages, npages, (npages + 2*grid - 1)/(2*grid), out); });
+  return 0;
+}
