@@ -7,7 +7,9 @@
 //     in flight);
 //   * rows: whole pages (33 contiguous KB) per wave, P loads in flight;
 //   * rows pipe: whole pages, the next page's 33 loads issued before the
-//     current one is consumed.
+//     current one is consumed;
+//   * dma: per-head cells by direct-to-LDS loads as the paged kernel issues
+//     them (C 16-key groups per chunk, D chunks in flight per wave).
 // Not part of the library: a measurement of the ceiling that the kernels'
 // roofline fractions are read against.
 //
@@ -24,6 +26,60 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4a __attribute__((ext_vector_type(4), aligned(4)));
 #define CK(x) do{hipError_t e=(x); if(e!=hipSuccess){printf("err %s line %d\n",hipGetErrorString(e),__LINE__);exit(1);}}while(0)
 constexpr int PAGE = 16 * 8 * 264;  // 33792 = 33 KB
+
+__device__ __forceinline__ void dma16(const char* g, char* lds) {
+  __builtin_amdgcn_global_load_lds((const void __attribute__((address_space(1)))*)(g),
+      (void __attribute__((address_space(3)))*)(lds), 16, 0, 0);
+}
+__device__ __forceinline__ void dma4(const char* g, char* lds) {
+  __builtin_amdgcn_global_load_lds((const void __attribute__((address_space(1)))*)(g),
+      (void __attribute__((address_space(3)))*)(lds), 4, 0, 0);
+}
+template <int N> __device__ __forceinline__ void wait_vm() { asm volatile("s_waitcnt vmcnt(%0)" :: "n"(N) : "memory"); }
+
+// DMA: per wave (= head) a sequence of 16-key groups (one page each). A "chunk" = C groups
+// (C = 1: 16 keys, 5 DMAs; C = 2: 32 keys, 9 DMAs). D chunks in flight.
+template <int C, int D, bool SWZ = false>
+__global__ __launch_bounds__(512) void rd_dma(const char* base, const int* pages, int npages, int per_wg, uint32_t* out) {
+  constexpr int SLOT = C * 16 * 264;
+  __shared__ __attribute__((aligned(16))) char lds_all[8 * D * SLOT];
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  char* lds = lds_all + wave * D * SLOT;
+  const int pb = blockIdx.x * per_wg, pe = min(npages, pb + per_wg);
+  const int tok = lane >> 3, piece = lane & 7;
+  uint32_t acc = 0;
+  auto issue = [&](int pg, char* slot) {
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      const int pgi = min(pg + c, pe - 1);
+      const char* page = base + (size_t)pages[pgi] * PAGE;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const char* cell = page + (size_t)(8 * h + tok) * 2112 + wave * 264;
+        const int pc = SWZ ? (piece ^ tok) : piece;
+        dma16(cell + 16 * pc, slot + c * 4096 + 1024 * h);
+        dma16(cell + 132 + 16 * pc, slot + c * 4096 + 2048 + 1024 * h);
+      }
+    }
+    // scales: lanes 0..15: ks of keys 0..15 of group 0, 16..31 vs; 32.. group 1 (C=2)
+    const int c = C == 2 ? (lane >> 5) : 0;
+    const int pgi = min(pg + c, pe - 1);
+    const char* page = base + (size_t)pages[pgi] * PAGE;
+    if (C == 2 || lane < 32)
+      dma4(page + (size_t)(lane & 15) * 2112 + wave * 264 + ((lane & 16) ? 260 : 128), slot + C * 4096);
+  };
+  int pg = pb, inflight = 0, slot_w = 0, slot_r = 0;
+  for (int i = 0; i < D && pg < pe; ++i) { issue(pg, lds + slot_w * SLOT); pg += C; ++inflight; slot_w = (slot_w + 1) % D; }
+  while (inflight > 0) {
+    if (inflight >= 2 && D >= 2) wait_vm<(C == 2 ? 9 : 5)>(); else wait_vm<0>();
+    uint32_t v;
+    asm volatile("ds_read_b32 %0, %1\n s_waitcnt lgkmcnt(0)" : "=v"(v) : "v"((uint32_t)(uintptr_t)(lds + slot_r * SLOT + 4 * lane)));
+    acc ^= v;
+    --inflight; slot_r = (slot_r + 1) % D;
+    if (pg < pe) { issue(pg, lds + slot_w * SLOT); pg += C; ++inflight; slot_w = (slot_w + 1) % D; }
+  }
+  if (acc == 0x12345678) out[0] = acc;
+}
 
 // per-head cell reads (the current kernel's pattern), register loads, U groups in flight
 template <int U>
@@ -124,6 +180,9 @@ int main() {
   timeit("rows P=11", [&]{ rd_rows<11><<<grid,512>>>(buf, pages, npages, per, out); });
   timeit("rows P=33", [&]{ rd_rows<33><<<grid,512>>>(buf, pages, npages, per, out); });
   timeit("rows pipe 2x33", [&]{ rd_rows_pipe<<<grid,512>>>(buf, pages, npages, per, out); });
+  timeit("dma C=2 D=1", [&]{ rd_dma<2,1><<<grid,512>>>(buf, pages, npages, per, out); });
+  timeit("dma C=2 D=2", [&]{ rd_dma<2,2><<<grid,512>>>(buf, pages, npages, per, out); });
+  timeit("dma C=2 D=2 swizzled", [&]{ rd_dma<2,2,true><<<grid,512>>>(buf, pages, npages, per, out); });
   timeit("rows P=11 grid x2", [&]{ rd_rows<11><<<2*grid,512>>>(buf, pages, npages, (npages + 2*grid - 1)/(2*grid), out); });
   return 0;
 }
