@@ -46,7 +46,7 @@
 #include "attn_device.h"
 
 #ifndef PA_PAGED_INFLIGHT
-#define PA_PAGED_INFLIGHT 2
+#define PA_PAGED_INFLIGHT 1
 #endif
 
 namespace pa {
@@ -55,9 +55,13 @@ namespace {
 // ---------------------------------------------------------------------------
 // Paged kernel (block size a multiple of 16): the 16-key halves of a chunk
 // each lie in one page. A producer walks this wave's chunk sequence -- all
-// chunks of its units, in order -- and keeps the next two in flight in the
-// wave's two LDS slots with direct-to-LDS loads; the consumer computes the
-// chunk before them from registers. The producer crosses unit boundaries, so
+// chunks of its units, in order -- and keeps the next PA_PAGED_INFLIGHT chunks
+// in flight in the wave's LDS slots with direct-to-LDS loads; the consumer
+// computes the chunk before them from registers. One slot is the default: the
+// consumer copies a chunk to registers, refills the slot and computes while
+// the next chunk loads. A second slot (two chunks in flight) measured 1-3 %
+// slower on the long-decode configurations: the deeper queue of DMA writes
+// into LDS costs more than the extra latency hiding buys. The producer crosses unit boundaries, so
 // a new unit's first chunks are already in flight while the previous unit
 // finishes: the pipeline does not drain between units.
 template <bool kWindow, bool kStream>
