@@ -11,10 +11,13 @@
 // or uninitialised memory) never enters an arithmetic operation; the sums run
 // in the fixed order s = 0..S-1, so the result is deterministic.
 //
-// Few rows with many splits (shared_rows): a work-group of 4 waves takes one
-// (token, head) row: wave 0 alone, or, for a row with more than 64 splits,
-// all 4 (wave w merges the 64-split blocks w, w + 4, ... and wave 0 merges
-// the 4 results in a fixed order). Otherwise one wave per row.
+// Few rows with many splits (shared_rows): a work-group of 16 waves takes one
+// (token, head) row (wave w merges the 16-split blocks w, w + 16, ... and
+// wave 0 merges the 16 results in a fixed order). Otherwise one wave per row.
+// The kernels are latency-bound, so the loads are ordered by round: the
+// padding bound, the split-count marker and the wave's LSEs are issued
+// together (the LSEs before their count is known; slots past it are then
+// dropped), then the partial rows of every split with a nonzero weight.
 // Lane l owns columns [l NC, (l + 1) NC), NC = D / 64, so a split's row is
 // one coalesced 4 D-byte read. Lane s loads lse_s (64 splits per instruction);
 // the weights are broadcast with readlane and the o loads of 16 splits are
@@ -98,20 +101,18 @@ __device__ __forceinline__ int row_live_splits(const CombineParams& c, int r, in
 // Splits of row (tok, head) on the op path: the count the attention kernel
 // recorded in the row's last log2-LSE slot (a quiet NaN with the count as
 // payload, attn_device.h), or all num_splits when the slot holds a real LSE.
-__device__ __forceinline__ int marked_splits(const CombineParams& c, int64_t tok, int head) {
-  const uint32_t bits = *reinterpret_cast<const uint32_t*>(
+__device__ __forceinline__ uint32_t marker_bits(const CombineParams& c, int64_t tok, int head) {
+  return *reinterpret_cast<const uint32_t*>(
       c.ws_lse + static_cast<int64_t>(c.num_splits - 1) * c.s_wl_split + tok * c.s_wl_tok +
       static_cast<int64_t>(head) * c.s_wl_head);
+}
+__device__ __forceinline__ int splits_of_marker(const CombineParams& c, uint32_t bits) {
   const uint32_t n = bits & 0x003fffffu;
   return (bits & 0xffc00000u) == 0x7fc00000u && n >= 1 && n < static_cast<uint32_t>(c.num_splits)
              ? static_cast<int>(n)
              : c.num_splits;
 }
 
-// Padding rows (tokens at or beyond qsl[R]) are never read or written.
-__device__ __forceinline__ bool padding_token(const CombineParams& c, int64_t tok) {
-  return tok >= ld_ro(c.qsl, c.num_reqs);
-}
 
 // NC consecutive fp32 columns at p (4 NC-byte aligned).
 template <int NC>
@@ -186,6 +187,66 @@ __device__ __forceinline__ void merge_blocks(const CombineParams& c, int64_t tok
   den = wave_sum(den_l);
 }
 
+// Merge of block `first` alone (every split of the row lies in the wave's
+// one block), with the block's log2-LSEs already loaded: x_spec is lane l's
+// slot kBlk first + l, read before the split count S was known, so lanes at
+// or past S drop it. Same arithmetic in the same order as merge_blocks, so
+// the results are identical; the partial rows are issued kOB at a time.
+template <int NC, int kBlk>
+__device__ __forceinline__ void merge_one_block(const CombineParams& c, int64_t tok, int head,
+                                                int S, int first, float x_spec, int lane,
+                                                float& M, float (&num)[NC], float& den) {
+  constexpr int kOB = kBatch<NC> < kBlk ? kBatch<NC> : kBlk;
+  const char* o_row =
+      c.ws_o + tok * c.s_wo_tok + static_cast<int64_t>(head) * c.s_wo_head + 4 * NC * lane;
+  const int s0 = kBlk * first;
+  const float x = lane < kBlk && s0 + lane < S ? x_spec : kNegInf;
+  M = wave_max(x > kNegInf ? x : kNegInf);  // NaN never wins
+#pragma unroll
+  for (int i = 0; i < NC; ++i) num[i] = 0.0f;
+  den = 0.0f;
+  if (!(M > kNegInf)) return;
+  const float w_l = x > kNegInf ? __builtin_amdgcn_exp2f(x - M) : 0.0f;
+  const int n = S - s0 < kBlk ? S - s0 : kBlk;
+  for (int e0 = 0; e0 < n; e0 += kOB) {
+    float w[kOB];
+    float ov[kOB][NC];
+#pragma unroll
+    for (int k = 0; k < kOB; ++k) {
+      const int e = e0 + k;
+      w[k] = e < n ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(
+                                                    __builtin_bit_cast(int, w_l), e))
+                   : 0.0f;
+      if (w[k] > 0.0f) {
+        load_cols<NC>(o_row + (s0 + e) * c.s_wo_split, ov[k]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < NC; ++i) ov[k][i] = 0.0f;
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < kOB; ++k) {
+      if (w[k] > 0.0f) {
+#pragma unroll
+        for (int i = 0; i < NC; ++i) num[i] = fmaf(w[k], ov[k][i], num[i]);
+      }
+    }
+  }
+  den = wave_sum(w_l);
+}
+
+// Lane l's log2-LSE slot kBlk first + l of row (tok, head), or -inf past the
+// launch's splits.
+template <int kBlk>
+__device__ __forceinline__ float lse_slot(const CombineParams& c, int64_t tok, int head, int first,
+                                          int lane) {
+  const int s = kBlk * first + lane;
+  if (lane >= kBlk || s >= c.num_splits) return kNegInf;
+  return *reinterpret_cast<const float*>(c.ws_lse + tok * c.s_wl_tok +
+                                         static_cast<int64_t>(head) * c.s_wl_head +
+                                         static_cast<int64_t>(s) * c.s_wl_split);
+}
+
 template <int NC>
 __device__ __forceinline__ void write_row(const CombineParams& c, int64_t tok, int head, float M,
                                           const float (&num)[NC], float den, int lane) {
@@ -241,13 +302,21 @@ __global__ __launch_bounds__(256) void combine_splits(const CombineParams c) {
   const int64_t tok = row / c.num_q_heads;
   const int head = static_cast<int>(row - tok * c.num_q_heads);
   if (tok >= c.num_tokens) return;
-  // Both loads in flight together.
-  const int S = c.seq_lens != nullptr ? marked_splits(c, tok, head) : c.num_splits;
-  if (padding_token(c, tok)) return;
+  // The marker, the padding bound and (when every split fits one 64-split
+  // block) the LSEs are loaded in one round.
+  const bool one_block = c.num_splits <= 64;
+  const int bound = ld_ro(c.qsl, c.num_reqs);
+  const uint32_t bits = marker_bits(c, tok, head);  // read on every path: the slot exists
+  const float x_spec = one_block ? lse_slot<64>(c, tok, head, 0, lane) : kNegInf;
+  if (tok >= bound) return;  // padding row
+  const int S = c.seq_lens != nullptr ? splits_of_marker(c, bits) : c.num_splits;
   if (c.seq_lens != nullptr && S == 1) return;  // written to out by the attention kernel
   float M, den;
   float num[NC];
-  merge_blocks<NC>(c, tok, head, S, 0, 1, lane, M, num, den);
+  if (one_block)
+    merge_one_block<NC, 64>(c, tok, head, S, 0, x_spec, lane, M, num, den);
+  else
+    merge_blocks<NC>(c, tok, head, S, 0, 1, lane, M, num, den);
   write_row<NC>(c, tok, head, M, num, den, lane);
 }
 
@@ -267,12 +336,22 @@ __global__ __launch_bounds__(kSharedWaves * 64) void combine_shared(const Combin
   const int64_t row = blockIdx.x;
   const int64_t tok = row / c.num_q_heads;
   const int head = static_cast<int>(row - tok * c.num_q_heads);
-  if (tok >= c.num_tokens || padding_token(c, tok)) return;  // uniform over the work-group
-  const int S = c.seq_lens != nullptr ? marked_splits(c, tok, head) : c.num_splits;
+  if (tok >= c.num_tokens) return;  // uniform over the work-group
+  // The padding bound, the marker and (when every split fits one block per
+  // wave) the wave's LSEs are loaded in one round.
+  const bool one_block = c.num_splits <= kSharedWaves * kSharedBlock;
+  const int bound = ld_ro(c.qsl, c.num_reqs);
+  const uint32_t bits = marker_bits(c, tok, head);  // read on every path: the slot exists
+  const float x_spec = one_block ? lse_slot<kSharedBlock>(c, tok, head, wave, lane) : kNegInf;
+  if (tok >= bound) return;  // padding row, uniform over the work-group
+  const int S = c.seq_lens != nullptr ? splits_of_marker(c, bits) : c.num_splits;
   if (c.seq_lens != nullptr && S == 1) return;  // written to out by the attention kernel
   float M, den;
   float num[NC];
-  merge_blocks<NC, kSharedBlock>(c, tok, head, S, wave, kSharedWaves, lane, M, num, den);
+  if (one_block)
+    merge_one_block<NC, kSharedBlock>(c, tok, head, S, wave, x_spec, lane, M, num, den);
+  else
+    merge_blocks<NC, kSharedBlock>(c, tok, head, S, wave, kSharedWaves, lane, M, num, den);
   if (lane == 0) {
     part_m[wave] = M;
     part_den[wave] = den;
