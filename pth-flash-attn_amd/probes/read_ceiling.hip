@@ -9,7 +9,8 @@
 //   * rows pipe: whole pages, the next page's 33 loads issued before the
 //     current one is consumed;
 //   * dma: per-head cells by direct-to-LDS loads as the paged kernel issues
-//     them (C 16-key groups per chunk, D chunks in flight per wave).
+//     them (C 16-key groups per chunk, D chunks in flight per wave, and a
+//     work-group barrier every BAR chunks when BAR > 0).
 // Not part of the library: a measurement of the ceiling that the kernels'
 // roofline fractions are read against.
 //
@@ -39,7 +40,7 @@ template <int N> __device__ __forceinline__ void wait_vm() { asm volatile("s_wai
 
 // DMA: per wave (= head) a sequence of 16-key groups (one page each). A "chunk" = C groups
 // (C = 1: 16 keys, 5 DMAs; C = 2: 32 keys, 9 DMAs). D chunks in flight.
-template <int C, int D, bool SWZ = false>
+template <int C, int D, bool SWZ = false, int BAR = 0>
 __global__ __launch_bounds__(512) void rd_dma(const char* base, const int* pages, int npages, int per_wg, uint32_t* out) {
   constexpr int SLOT = C * 16 * 264;
   __shared__ __attribute__((aligned(16))) char lds_all[8 * D * SLOT];
@@ -77,6 +78,7 @@ __global__ __launch_bounds__(512) void rd_dma(const char* base, const int* pages
     acc ^= v;
     --inflight; slot_r = (slot_r + 1) % D;
     if (pg < pe) { issue(pg, lds + slot_w * SLOT); pg += C; ++inflight; slot_w = (slot_w + 1) % D; }
+    if (BAR > 0 && ((pg - pb) / C) % BAR == 0) __builtin_amdgcn_s_barrier();
   }
   if (acc == 0x12345678) out[0] = acc;
 }
@@ -183,6 +185,7 @@ int main() {
   timeit("dma C=2 D=1", [&]{ rd_dma<2,1><<<grid,512>>>(buf, pages, npages, per, out); });
   timeit("dma C=2 D=2", [&]{ rd_dma<2,2><<<grid,512>>>(buf, pages, npages, per, out); });
   timeit("dma C=2 D=2 swizzled", [&]{ rd_dma<2,2,true><<<grid,512>>>(buf, pages, npages, per, out); });
+  timeit("dma C=2 D=1, barrier every 8 chunks", [&]{ rd_dma<2,1,false,8><<<grid,512>>>(buf, pages, npages, per, out); });
   timeit("rows P=11 grid x2", [&]{ rd_rows<11><<<2*grid,512>>>(buf, pages, npages, (npages + 2*grid - 1)/(2*grid), out); });
   return 0;
 }
