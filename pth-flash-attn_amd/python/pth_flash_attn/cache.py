@@ -83,6 +83,46 @@ def carve_views(
     return k, v, ks, vs
 
 
+def vllm_packed_views(
+    kv_packed: torch.Tensor,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+    """The op's (k_cache, v_cache, k_scale, v_scale) views of vLLM's packed
+    ``int8_per_token_head`` layer cache.
+
+    vLLM keeps one int8 tensor per layer, logically ``[blocks, kv_heads,
+    block_size, 2 (D + 4)]``: per (block, head, slot) the cell ``[K | k_scale |
+    V | v_scale]`` (reference docs/integration.md:40-46, pth_testing/
+    reference.py:268-300). The views index ``[block, slot, head]`` with the
+    strides of the tensor itself (never derived from its shape), so padded or
+    strided caches work; nothing is copied.
+    """
+    if kv_packed.dtype != torch.int8 or kv_packed.dim() != 4:
+        raise ValueError("kv_packed must be an int8 tensor [blocks, kv_heads, block_size, 2 (D + 4)]")
+    nb, hkv, bs, content = kv_packed.shape
+    if content % 2 or content // 2 <= SCALE_BYTES:
+        raise ValueError(f"cell of {content} bytes is not 2 (D + 4)")
+    half = content // 2
+    D = half - SCALE_BYTES
+    s_blk, s_head, s_slot, s_byte = (int(x) for x in kv_packed.stride())
+    if s_byte != 1:
+        raise ValueError("the cell bytes of kv_packed must be contiguous")
+    if any(x % SCALE_BYTES for x in (s_blk, s_head, s_slot, kv_packed.storage_offset(), D)):
+        raise ValueError("kv_packed strides, offset and D must be multiples of 4 bytes")
+    base = kv_packed.storage_offset()
+    size = (nb, bs, hkv)
+    stride = (s_blk, s_slot, s_head)
+    k = torch.as_strided(kv_packed, (*size, D), (*stride, 1), base)
+    v = torch.as_strided(kv_packed, (*size, D), (*stride, 1), base + half)
+    f32 = torch.tensor([], dtype=torch.float32, device=kv_packed.device).set_(
+        kv_packed.untyped_storage()
+    )
+    w = SCALE_BYTES
+    stride_w = tuple(x // w for x in stride)
+    ks = torch.as_strided(f32, size, stride_w, (base + D) // w)
+    vs = torch.as_strided(f32, size, stride_w, (base + half + D) // w)
+    return k, v, ks, vs
+
+
 @dataclass
 class PagedCache:
     """A filled cache plus the per-request metadata the op needs."""

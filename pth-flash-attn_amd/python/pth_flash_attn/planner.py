@@ -38,10 +38,10 @@ kernel holds 2 waves per SIMD (<= 256 VGPRs), 4 SIMDs per CU, so one CU keeps
 8 units resident: CTAS_PER_SM[128] = 8 and C_target = 256 CUs * 8 = 2048 on
 MI355X. The kernel itself uses only as many of the S splits as a row tile's
 length needs (at least 4 KV tiles per split, read on the device), so a large S
-costs empty work-groups, not combine traffic. D = 64 and 256 have no gfx950
-kernel yet; their entries are the register-budget estimates (the D = 64 unit
-would fit 2 waves/SIMD as well, the D = 256 unit 1) and only matter to the
-planner's arithmetic.
+costs empty work-groups, not combine traffic. D = 64 and 256 run on the
+register-load kernel (8 waves per CU as well). Their entries only size the
+split count: 8 for D = 64; 4 for D = 256, whose units read twice the bytes per
+key, so half as many splits already keep the CUs' loads in flight.
 """
 
 from __future__ import annotations
