@@ -18,6 +18,9 @@ layer-call), and
   cpu_baseline - the repository's CPU oracle (fp64 restatement of the
                  reference's CPU path) on a bounded sample of the same workload.
 
+Warm-up: W untimed steps, continued until they add up to at least 0.3 s of
+GPU work (the step count run is printed as warmup_steps_run).
+
 Usage: python bench.py [--steps K] [--warmup W] [--config 1..5] [--no-cpu]
 """
 
@@ -40,6 +43,9 @@ PEAK_BF16_TFLOPS = 2500.0
 METRIC = "µs/layer-call + achieved HBM GB/s (% peak), int8 paged decode D=128"
 CELL = 264  # bytes per (token, KV head): K 128 + k_scale 4 + V 128 + v_scale 4
 
+
+# Untimed warm-up lasts at least this long (seconds of GPU work), W steps at least.
+WARMUP_MIN_S = 0.3
 
 def workload(config: int):
     """(name, q_lens, seq_lens, Hq, Hkv, window, is_prefill) of a BASELINE config."""
@@ -222,8 +228,16 @@ def main() -> int:
                                ws_o, ws_lse, window, True)
 
     stream = torch.cuda.current_stream()
-    for _ in range(a.warmup):
+    # Untimed warm-up: the W steps asked for, continued until they add up to
+    # WARMUP_MIN_S of GPU work, so that the first timed steps do not run while
+    # the clocks and the TLBs settle (about 4 % slower on config 2 after 4 ms).
+    warm_t0 = time.perf_counter()
+    warm_steps = 0
+    while warm_steps < a.warmup or time.perf_counter() - warm_t0 < WARMUP_MIN_S:
         step()
+        warm_steps += 1
+        if warm_steps % 10 == 0:
+            torch.cuda.synchronize()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -268,6 +282,7 @@ def main() -> int:
         "n_gpus": 1,
         "steps": a.steps,
         "warmup": a.warmup,
+        "warmup_steps_run": warm_steps,
         "ms_per_step": round(ms, 5),
         "us_per_layer_call": round(ms * 1e3, 2),
         "pct_of_peak_hbm": round(100.0 * gbs / PEAK_HBM_GBS, 2),
