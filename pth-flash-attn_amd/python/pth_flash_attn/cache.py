@@ -96,8 +96,11 @@ def vllm_packed_views(
     strides of the tensor itself (never derived from its shape), so padded or
     strided caches work; nothing is copied.
     """
+    if kv_packed.dtype == torch.uint8:
+        kv_packed = kv_packed.view(torch.int8)  # the same bytes
     if kv_packed.dtype != torch.int8 or kv_packed.dim() != 4:
-        raise ValueError("kv_packed must be an int8 tensor [blocks, kv_heads, block_size, 2 (D + 4)]")
+        raise ValueError("kv_packed must be an int8 (or uint8) tensor "
+                         "[blocks, kv_heads, block_size, 2 (D + 4)]")
     nb, hkv, bs, content = kv_packed.shape
     if content % 2 or content // 2 <= SCALE_BYTES:
         raise ValueError(f"cell of {content} bytes is not 2 (D + 4)")

@@ -388,9 +388,16 @@ def test_vllm_packed_views_equal_the_hnd_cell_views(pad, D_):
     assert all(torch.equal(a, b) for a, b in zip(got, ref))
 
 
+def test_vllm_packed_views_accept_uint8_storage():
+    packed = torch.randint(0, 256, (3, 2, 16, 264), dtype=torch.uint8)
+    got = vllm_packed_views(packed)
+    want = vllm_packed_views(packed.view(torch.int8))
+    assert all(torch.equal(a, b) and a.dtype == b.dtype for a, b in zip(got, want))
+
+
 def test_vllm_packed_views_refuse_bad_layouts():
     with pytest.raises(ValueError):
-        vllm_packed_views(torch.zeros(2, 2, 16, 264, dtype=torch.uint8))
+        vllm_packed_views(torch.zeros(2, 2, 16, 264, dtype=torch.float16))
     with pytest.raises(ValueError):
         vllm_packed_views(torch.zeros(2, 2, 16, 263, dtype=torch.int8))
     with pytest.raises(ValueError):
