@@ -186,6 +186,8 @@ int main() {
   timeit("dma C=2 D=2", [&]{ rd_dma<2,2><<<grid,512>>>(buf, pages, npages, per, out); });
   timeit("dma C=2 D=2 swizzled", [&]{ rd_dma<2,2,true><<<grid,512>>>(buf, pages, npages, per, out); });
   timeit("dma C=2 D=1, barrier every 8 chunks", [&]{ rd_dma<2,1,false,8><<<grid,512>>>(buf, pages, npages, per, out); });
+  timeit("dma C=2 D=1, 2 work-groups per CU", [&]{ rd_dma<2,1><<<2*grid,512>>>(buf, pages, npages, (npages + 2*grid - 1)/(2*grid), out); });
+  timeit("dma C=2 D=1, 3 work-groups per CU", [&]{ rd_dma<2,1><<<3*grid,512>>>(buf, pages, npages, (npages + 3*grid - 1)/(3*grid), out); });
   timeit("rows P=11 grid x2", [&]{ rd_rows<11><<<2*grid,512>>>(buf, pages, npages, (npages + 2*grid - 1)/(2*grid), out); });
   return 0;
 }
