@@ -208,8 +208,11 @@ PA_HD void request_chunks(int32_t q_len, int32_t seq_len, int32_t bq, int32_t wi
 // Stream positions per work-group: an even share of `total`, but at least
 // kMinChunksPerSplit and enough that no stream of up to `max_n` chunks
 // meets more than num_splits work-groups (a stream of n chunks meets at most
-// ceil((n - 1) / per) + 1 of them).
-constexpr int32_t kMinChunksPerSplit = 4;
+// ceil((n - 1) / per) + 1 of them). One chunk is the floor: a small launch
+// is a chain of dependent chunk loads per wave, so the shortest chain wins
+// (measured: config 1's layer call 20.3 us with a floor of 4 chunks, 16.5 us
+// with 1; long launches have shares far above the floor).
+constexpr int32_t kMinChunksPerSplit = 1;
 PA_HD int64_t chunks_per_group(int64_t total, int32_t max_n, int32_t num_wg, int32_t num_splits) {
   int64_t per = (total + num_wg - 1) / num_wg;
   if (per < kMinChunksPerSplit) per = kMinChunksPerSplit;

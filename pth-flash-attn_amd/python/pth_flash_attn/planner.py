@@ -37,7 +37,7 @@ kernel: (row tile, KV head, 16-row group, split), run by one wave64. The D=128
 kernel holds 2 waves per SIMD (<= 256 VGPRs), 4 SIMDs per CU, so one CU keeps
 8 units resident: CTAS_PER_SM[128] = 8 and C_target = 256 CUs * 8 = 2048 on
 MI355X. The kernel itself uses only as many of the S splits as a row tile's
-length needs (at least 4 KV tiles per split, read on the device), so a large S
+length needs (read on the device; at least one 32-key chunk per split), so a large S
 costs empty work-groups, not combine traffic. D = 64 and 256 run on the
 register-load kernel (8 waves per CU as well). Their entries only size the
 split count: 8 for D = 64; 4 for D = 256, whose units read twice the bytes per

@@ -392,7 +392,11 @@ def test_vllm_packed_views_accept_uint8_storage():
     packed = torch.randint(0, 256, (3, 2, 16, 264), dtype=torch.uint8)
     got = vllm_packed_views(packed)
     want = vllm_packed_views(packed.view(torch.int8))
-    assert all(torch.equal(a, b) and a.dtype == b.dtype for a, b in zip(got, want))
+
+    def bits(t):  # random bytes may form NaN scales: compare bit patterns
+        return t.view(torch.int32) if t.dtype == torch.float32 else t
+
+    assert all(a.dtype == b.dtype and torch.equal(bits(a), bits(b)) for a, b in zip(got, want))
 
 
 def test_vllm_packed_views_refuse_bad_layouts():
