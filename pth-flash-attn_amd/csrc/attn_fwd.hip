@@ -174,6 +174,31 @@ void attn_fwd_paged(const AttnParams p) {
   P.U.n_chunks = 0;
   P.k = 0;
   P.done = false;
+  Work<kWindow, kStream> work = P.work;  // the consumer's walk: the same units, behind
+  Unit U;
+  Lanes L;
+  State st;
+  bf16x8 qb[4], qlo[4];
+  int ck = 0;
+  bool have = false;
+  int slot_r = 0;
+  // The consumer's first unit is located, and its query load issued, before
+  // the producer's first chunk: the two loads are in flight together (a
+  // short launch is a chain of dependent loads per wave).
+  while (work.next(p, lane, U)) {
+    if (!U.has_rows) continue;
+    L = unit_lanes<kWindow>(p, U, lane);
+    if (U.n_chunks == 0) {  // no key of these rows in this split
+      State empty;
+      state_reset(empty);
+      epilogue(p, U, L, empty);
+      continue;
+    }
+    have = true;
+    break;
+  }
+  if (have) load_q<kF16Q>(p, L, qb, qlo);
+
   int inflight = 0;  // chunks issued and not yet consumed
   int slot_w = 0;    // slot the producer fills next
 #pragma unroll
@@ -184,16 +209,10 @@ void attn_fwd_paged(const AttnParams p) {
       slot_w = slot_w + 1 == kInFlight ? 0 : slot_w + 1;
     }
   }
-
-  Work<kWindow, kStream> work;  // the consumer's walk: the same units, behind
-  work.init(p, lane);
-  Unit U;
-  Lanes L;
-  State st;
-  bf16x8 qb[4], qlo[4];
-  int ck = 0;
-  bool have = false;
-  int slot_r = 0;
+  // Compiler-visible wait for the query (it also waits for the chunks just
+  // issued, which the first step needs anyway).
+  __builtin_amdgcn_s_waitcnt(0x0F70);
+  state_reset(st);
   // The stores of a finished unit are issued after the wait that drains the
   // pipeline at the unit switch: vector memory operations complete in issue
   // order, so a store issued in front of chunks still in flight would make
