@@ -1,18 +1,19 @@
 // attn_fwd.hip -- the gfx950 paged int8 attention kernel, D = 128.
 //
-// Work decomposition. A work unit is (request, row tile, split, KV head,
-// 16-row group); a row tile holds up to bq query tokens of one request and
-// its rows are (token, head-in-group) pairs, token-major (reference
-// cache_geometry.cuh:319-334). The kernel is persistent: the grid is one
-// wave64 per resident slot of the GPU (CUs x 8) and wave w runs units
-// w, w + W, w + 2W, ... of a table that it derives on the device from
-// query_start_loc and seq_lens (a prefix sum over requests, 64 requests per
-// wave instruction), so the launch is graph-safe and no work-group is ever
-// spent on an empty split. Each request uses as many splits as its length
-// needs (at least 4 KV tiles each, at most the planner's S). The KV head is
-// the fastest index of the table: the 4 waves of a work-group take 4 adjacent
-// heads of one (row tile, split), whose cache cells are adjacent in memory,
-// so the lines they share are fetched into L2 once.
+// Work decomposition. A work unit is (request, row tile, KV head, 16-row
+// group) over a range of keys; a row tile holds up to bq query tokens of one
+// request and its rows are (token, head-in-group) pairs, token-major
+// (reference cache_geometry.cuh:319-334). The kernels are persistent and
+// derive their work on the device from query_start_loc and seq_lens, so a
+// launch is graph-safe (Work in attn_device.h). With one split, wave w of
+// the grid takes units w, w + W, ... of a table built by a prefix sum over
+// the requests. With S > 1, the 32-key chunk streams of every (row tile,
+// group of 8 KV-head units) are laid end to end and work-group b takes the
+// positions [b per, (b + 1) per) (attn_geometry.h, attn_stream.h), so every
+// work-group has the same work and a stream has as many splits as the
+// work-groups it meets (at most the planner's S). The 8 waves of a
+// work-group take the 8 units of a group: with 8 KV heads, the 8 heads of
+// the same keys, whose cells are adjacent in memory and share cache lines.
 //
 // MFMA layout ("swap AB"). Both products use v_mfma_f32_16x16x32_bf16 with the
 // keys on the M side and the 16 query rows on N:
@@ -40,8 +41,9 @@
 // needed (they exist for fp16's range).
 //
 // Softmax. Scores are in log2 units (scale * log2 e folded in); the running
-// max is reduced over the 4 lanes of a row with two xor shuffles; the
-// running sum stays per lane and is reduced once at the end.
+// max is reduced over the 4 lanes of a row with the gfx950 cross-row swaps
+// (permlane16/32); the running sum stays per lane and is reduced once at the
+// end.
 
 #include "attn_device.h"
 

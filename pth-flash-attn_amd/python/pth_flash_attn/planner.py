@@ -133,8 +133,10 @@ def split_tile_range(*, split: int, num_splits: int, num_tiles: int) -> tuple[in
     """KV-tile range [start, end) of split ``split``: [s T / S, (s + 1) T / S).
 
     Ranges are disjoint, cover [0, T) and differ by at most one tile; when
-    T < S some are empty. The kernel applies this partition with S replaced by
-    the split count the row tile actually uses (at least 4 tiles per split).
+    T < S some are empty. This is the reference's per-row-tile partition,
+    kept as its interface; the gfx950 kernels cut the chunk streams of all
+    row tiles into equal ranges per work-group instead (at most S per row
+    tile).
     """
     total = _host_int("num_splits", num_splits, 1)
     s = _host_int("split", split, 0)
