@@ -288,6 +288,22 @@ def test_public_entry_points_combine_all_splits(S):
     assert_parity(res, name=f"public S={S}", strict=False)
 
 
+@pytest.mark.parametrize("S", [5, 34])
+@pytest.mark.parametrize("causal", [True, False])
+def test_public_entry_points_windowed_verify(S, causal):
+    """As above for windowed verify rows of more than 16 rows per KV head
+    (the work units of 32 rows): the unused-split fill and the combine must
+    use the attention launch's partition."""
+    c = Case("public-window", q_lens=[16, 8, 3], seq_lens=[3000, 700, 40], window=512,
+             causal=causal, seed=22)
+    b = materialize(c, DEV)
+    out, _ = run_capi(b, num_splits=S, with_lse=False)
+    ref_out, ref_lse, valid = oracle_of(b)
+    res = compare(out, None, ref_out, ref_lse, valid)
+    print(f"  S={S} causal={causal} -> {res}", flush=True)
+    assert_parity(res, name=f"public window S={S}", strict=False)
+
+
 # ---------------------------------------------------------------- configs 2-5
 def test_config2_batched_decode():
     """Config 2: 64 seqs, q=1, 32q/8kv, L ~ U[1k, 32k], BS 16."""
