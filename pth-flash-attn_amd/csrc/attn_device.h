@@ -92,6 +92,15 @@ __device__ __forceinline__ float max_raw(float a, float b) {
   asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
   return r;
 }
+__device__ __forceinline__ float max3_raw(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+// Max of a lane's 8 scores (finite or -inf, never NaN) in 4 instructions.
+__device__ __forceinline__ float max8_raw(const float (&t)[8]) {
+  return max3_raw(max3_raw(t[0], t[1], t[2]), max3_raw(t[3], t[4], t[5]), max_raw(t[6], t[7]));
+}
 __device__ __forceinline__ float xor_max(float x) {
   const SwapPair a = swap_rows16(x);
   const SwapPair b = swap_halves(max_raw(a.a, a.b));
@@ -164,6 +173,29 @@ template <int N>
 __device__ __forceinline__ float row_bcast(float x) {
   return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x),
                                                             0x150 + N, 0xf, 0xf, false));
+}
+
+// The chunk's 8 K scales (times scale * log2 e) and 8 V scales of a lane,
+// from sc1 = (the lane's slot scale) * (scale * log2 e for K lanes, 1 for V):
+// lane r16 < 8 of a row holds the K scale of key 16 (r16 / 4) + 4 g + r16 % 4,
+// lane 8 + e the V scale of the same key.
+__device__ __forceinline__ void lane_scales(float sc1, float (&ks)[8], float (&vs)[8]) {
+  ks[0] = row_bcast<0>(sc1);
+  ks[1] = row_bcast<1>(sc1);
+  ks[2] = row_bcast<2>(sc1);
+  ks[3] = row_bcast<3>(sc1);
+  ks[4] = row_bcast<4>(sc1);
+  ks[5] = row_bcast<5>(sc1);
+  ks[6] = row_bcast<6>(sc1);
+  ks[7] = row_bcast<7>(sc1);
+  vs[0] = row_bcast<8>(sc1);
+  vs[1] = row_bcast<9>(sc1);
+  vs[2] = row_bcast<10>(sc1);
+  vs[3] = row_bcast<11>(sc1);
+  vs[4] = row_bcast<12>(sc1);
+  vs[5] = row_bcast<13>(sc1);
+  vs[6] = row_bcast<14>(sc1);
+  vs[7] = row_bcast<15>(sc1);
 }
 
 __device__ __forceinline__ const char* at(const CacheStream& s, int64_t page,
@@ -444,6 +476,13 @@ __device__ __forceinline__ void state_reset(StateT<D>& st) {
 // visible key always sets m.
 constexpr float kRescaleSlack = 8.0f;
 
+// A row's m moves when its chunk max exceeds this: kRescaleSlack, or for a
+// row with no visible key yet (m = -inf) any visible score (a score is
+// finite, so > -FLT_MAX is the same test as > -inf; one compare either way).
+__device__ __forceinline__ float rescale_threshold(bool fresh) {
+  return fresh ? -3.402823466e38f : kRescaleSlack;
+}
+
 // The operands of a chunk in registers as the D = 128 paged kernels load
 // them (Chunk); ops.k(sub, j) / ops.v(j) give the bf16 K and V operands and
 // ops.sc the lane's scale.
@@ -497,11 +536,8 @@ __device__ __forceinline__ void compute_chunk_t(const Unit& U, const Lanes& L, i
       }
     }
   }
-  float mx = t[0];
-#pragma unroll
-  for (int e = 1; e < 8; ++e) mx = fmaxf(mx, t[e]);
-  mx = xor_max(mx);
-  const bool grow = fresh ? mx > kNegInf : mx > kRescaleSlack;
+  const float mx = xor_max(max8_raw(t));
+  const bool grow = mx > rescale_threshold(fresh);
   if (__ballot(grow) != 0) {
     // Rows that keep m (also rows with no visible key yet) scale by 1.
     const float alpha = grow && !fresh ? __builtin_amdgcn_exp2f(-mx) : 1.0f;

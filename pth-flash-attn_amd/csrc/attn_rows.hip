@@ -253,13 +253,8 @@ template <bool kF16Q, class Ops>
 __device__ __forceinline__ void compute_rows(const RowSet& R, const Lanes (&L)[2], int c, Ops& ops,
                                              const bf16x8 (&qb)[2][4], const bf16x8 (&qlo)[2][4],
                                              float scl, State (&st)[2]) {
-  const float sc1 = ops.sc() * scl;
-  const float ks[8] = {row_bcast<0>(sc1), row_bcast<1>(sc1), row_bcast<2>(sc1),
-                       row_bcast<3>(sc1), row_bcast<4>(sc1), row_bcast<5>(sc1),
-                       row_bcast<6>(sc1), row_bcast<7>(sc1)};
-  float vs[8] = {row_bcast<8>(sc1),  row_bcast<9>(sc1),  row_bcast<10>(sc1),
-                 row_bcast<11>(sc1), row_bcast<12>(sc1), row_bcast<13>(sc1),
-                 row_bcast<14>(sc1), row_bcast<15>(sc1)};
+  float ks[8], vs[8];
+  ops.scales(scl, ks, vs);
   const int ng = R.two ? 2 : 1;
   bool fresh[2];
   float m_use[2];
@@ -269,6 +264,10 @@ __device__ __forceinline__ void compute_rows(const RowSet& R, const Lanes (&L)[2
     m_use[i] = fresh[i] ? 0.0f : st[i].m;
   }
   float t[2][8];
+  // The QK MFMAs run at raised wave priority: the SIMD's other wave, in its
+  // softmax, fills the VALU slots between them (measured -2.5 % on a mixed
+  // prefill launch; raising it for the PV products as well gained nothing).
+  __builtin_amdgcn_s_setprio(1);
 #pragma unroll
   for (int sub = 0; sub < 2; ++sub) {
     f32x4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
@@ -288,6 +287,7 @@ __device__ __forceinline__ void compute_rows(const RowSet& R, const Lanes (&L)[2
 #pragma unroll
       for (int e = 0; e < 4; ++e) t[i][4 * sub + e] = fmaf(acc[i][e], ks[4 * sub + e], -m_use[i]);
   }
+  __builtin_amdgcn_s_setprio(0);
   ops.load_v();
   if (c < R.w_lo_max || c + kChunkTokens - 1 > R.w_hi_min) {
     // Keys outside a row's range get p = 0; keys outside every row's range
@@ -306,11 +306,8 @@ __device__ __forceinline__ void compute_rows(const RowSet& R, const Lanes (&L)[2
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     if (i >= ng) continue;
-    float mx = t[i][0];
-#pragma unroll
-    for (int e = 1; e < 8; ++e) mx = fmaxf(mx, t[i][e]);
-    mx = xor_max(mx);
-    const bool grow = fresh[i] ? mx > kNegInf : mx > kRescaleSlack;
+    const float mx = xor_max(max8_raw(t[i]));
+    const bool grow = mx > rescale_threshold(fresh[i]);
     if (__ballot(grow) != 0) {
       const float alpha = grow && !fresh[i] ? __builtin_amdgcn_exp2f(-mx) : 1.0f;
       st[i].l *= alpha;
@@ -379,6 +376,9 @@ __device__ __forceinline__ uint32_t ds_read_i8(uint32_t a) {
   asm volatile("ds_read_i8 %0, %1" : "=v"(v) : "v"(a));
   return v;
 }
+__device__ __forceinline__ void ds_write4(uint32_t a, float v) {
+  asm volatile("ds_write_b32 %0, %1" ::"v"(a), "v"(v) : "memory");
+}
 template <int kOff>
 __device__ __forceinline__ void ds_write16(uint32_t a, u32x4 v) {
   asm volatile("ds_write_b128 %0, %1 offset:%2" ::"v"(a), "v"(v), "n"(kOff) : "memory");
@@ -402,7 +402,15 @@ __device__ __forceinline__ ConvOffsets conv_offsets(int wave, int lane) {
 
 // Wave `wave`'s eighth of the chunk in int8 slot `slot` -> bf16 copy `copy`.
 __device__ __forceinline__ void convert_share(uint32_t slot, uint32_t copy, const ConvOffsets& o,
-                                              int wave, int lane) {
+                                              float scale_log2, int wave, int lane) {
+  if (wave == kRowWaves - 1 && lane < kChunkTokens) {
+    // The chunk's K scales, in place: times scale * log2 e (the product the
+    // chunk step would form per lane).
+    const uint32_t sa = slot + kSlotScale + 4 * lane;
+    float x = ds_read4(sa);
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(x) : : "memory");
+    ds_write4(sa, x * scale_log2);
+  }
   u32x2 kw = ds_read8<0>(slot + o.k);
   uint32_t vb[8];
 #pragma unroll
@@ -431,7 +439,9 @@ __device__ __forceinline__ void convert_share(uint32_t slot, uint32_t copy, cons
 // Operands of compute_rows from the int8 chunk in registers.
 struct Int8Ops {
   const Chunk& ch;
-  __device__ __forceinline__ float sc() const { return ch.sc; }
+  __device__ __forceinline__ void scales(float scl, float (&ks)[8], float (&vs)[8]) const {
+    lane_scales(ch.sc * scl, ks, vs);
+  }
   __device__ __forceinline__ bf16x8 k(int sub, int j) const {
     const u32x4& w = ch.k[sub][j >> 1];
     return (j & 1) ? i8x8_to_bf16(w[2], w[3]) : i8x8_to_bf16(w[0], w[1]);
@@ -440,16 +450,24 @@ struct Int8Ops {
   __device__ __forceinline__ bf16x8 v(int j) const { return column_to_bf16(ch.v, j); }
 };
 
-// Operands of compute_rows from a bf16 copy: K and the scale read at
-// construction, V read by load_v.
+// Operands of compute_rows from a bf16 copy: K and the scales read at
+// construction, V read by load_v. The chunk's K scales in its int8 slot were
+// multiplied by scale * log2 e when it was converted (convert_share), so a
+// lane reads its 8 K and 8 V scales as they are: keys 4 g .. 4 g + 3 and
+// 16 + 4 g .., four 16-byte reads that the 16 lanes of a row share.
 struct CopyOps {
   uint32_t a;  // copy + 16 lane
   u32x4 kk[8];
   u32x4 vv[8];
-  float s;
+  u32x4 sk[2], sv[2];
 
-  __device__ __forceinline__ CopyOps(uint32_t copy, uint32_t scale_addr, int lane)
+  __device__ __forceinline__ CopyOps(uint32_t copy, uint32_t slot, int lane)
       : a(copy + lane * 16) {
+    const uint32_t sa = slot + kSlotScale + 16 * (lane >> 4);
+    sk[0] = ds_read16<0>(sa);
+    sk[1] = ds_read16<64>(sa);
+    sv[0] = ds_read16<128>(sa);
+    sv[1] = ds_read16<192>(sa);
     kk[0] = ds_read16<0>(a);
     kk[1] = ds_read16<1024>(a);
     kk[2] = ds_read16<2048>(a);
@@ -458,14 +476,22 @@ struct CopyOps {
     kk[5] = ds_read16<5120>(a);
     kk[6] = ds_read16<6144>(a);
     kk[7] = ds_read16<7168>(a);
-    s = ds_read4(scale_addr);
     asm volatile("s_waitcnt lgkmcnt(0)"
                  : "+v"(kk[0]), "+v"(kk[1]), "+v"(kk[2]), "+v"(kk[3]), "+v"(kk[4]), "+v"(kk[5]),
-                   "+v"(kk[6]), "+v"(kk[7]), "+v"(s)
+                   "+v"(kk[6]), "+v"(kk[7]), "+v"(sk[0]), "+v"(sk[1]), "+v"(sv[0]), "+v"(sv[1])
                  :
                  : "memory");
   }
-  __device__ __forceinline__ float sc() const { return s; }
+  __device__ __forceinline__ void scales(float, float (&ks)[8], float (&vs)[8]) const {
+    // Each element goes through a named scalar: a bit cast of a subscripted
+    // vector element reads element 0 with this compiler.
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const uint32_t kw = sk[e >> 2][e & 3], vw = sv[e >> 2][e & 3];
+      ks[e] = __builtin_bit_cast(float, kw);
+      vs[e] = __builtin_bit_cast(float, vw);
+    }
+  }
   __device__ __forceinline__ bf16x8 k(int sub, int j) const {
     return __builtin_bit_cast(bf16x8, kk[4 * sub + j]);
   }
@@ -611,8 +637,8 @@ __device__ __forceinline__ void wide_block(const AttnParams& p, const Block& B, 
     wait_vmcnt_dyn(nload * younger);
   }
   wg_barrier();
-  convert_share(lds_base + slot_of(0), copy0 + copy_of(0), cvo, wave, lane);
-  if (1 < len) convert_share(lds_base + slot_of(1), copy0 + copy_of(1), cvo, wave, lane);
+  convert_share(lds_base + slot_of(0), copy0 + copy_of(0), cvo, p.scale_log2, wave, lane);
+  if (1 < len) convert_share(lds_base + slot_of(1), copy0 + copy_of(1), cvo, p.scale_log2, wave, lane);
   for (int k = 0; k < len; k += 2) {
     if (k + 2 < len) {
       // Issued so far: chunks up to min(k + 5, len - 1); k + 2, k + 3 must land.
@@ -626,14 +652,14 @@ __device__ __forceinline__ void wide_block(const AttnParams& p, const Block& B, 
       issue_wide(p, Ld, pp, 0, lds + slot_of(k + 6), wave, lane);
       if (k + 7 < len) issue_wide(p, Ld, pp, 1, lds + slot_of(k + 7), wave, lane);
     }
-    if (k + 2 < len) convert_share(lds_base + slot_of(k + 2), copy0 + copy_of(k + 2), cvo, wave, lane);
-    if (k + 3 < len) convert_share(lds_base + slot_of(k + 3), copy0 + copy_of(k + 3), cvo, wave, lane);
+    if (k + 2 < len) convert_share(lds_base + slot_of(k + 2), copy0 + copy_of(k + 2), cvo, p.scale_log2, wave, lane);
+    if (k + 3 < len) convert_share(lds_base + slot_of(k + 3), copy0 + copy_of(k + 3), cvo, p.scale_log2, wave, lane);
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int kk = k + h;
       const int c = chunk_key(kk);
       if (kk < len && R.has_rows && c <= R.w_hi_max && c + kChunkTokens > R.w_lo_min) {
-        CopyOps ops(copy0 + copy_of(kk), lds_base + slot_of(kk) + ro.s, lane);
+        CopyOps ops(copy0 + copy_of(kk), lds_base + slot_of(kk), lane);
         compute_rows<kF16Q>(R, L, c, ops, qb, qlo, scl, st);
       }
     }
