@@ -249,13 +249,16 @@ __device__ __forceinline__ int rows_chunk_loads(int mask, int rs) {
 // the bf16 operands (converted from the int8 chunk, or read from the
 // work-group's converted copy): ops.sc() the lane's scale, ops.k(sub, j),
 // ops.load_v() (issued before the softmax) and ops.v(j).
-template <bool kF16Q, class Ops>
+// kBoth: compute both groups whether or not the second has rows (the wide
+// path: group 1 of a wave without rows repeats group 0 and is dropped). No
+// branch then separates the MFMAs (-5 % on a mixed prefill launch).
+template <bool kF16Q, bool kBoth, class Ops>
 __device__ __forceinline__ void compute_rows(const RowSet& R, const Lanes (&L)[2], int c, Ops& ops,
                                              const bf16x8 (&qb)[2][4], const bf16x8 (&qlo)[2][4],
                                              float scl, State (&st)[2]) {
   float ks[8], vs[8];
   ops.scales(scl, ks, vs);
-  const int ng = R.two ? 2 : 1;
+  const int ng = kBoth || R.two ? 2 : 1;
   bool fresh[2];
   float m_use[2];
 #pragma unroll
@@ -660,7 +663,7 @@ __device__ __forceinline__ void wide_block(const AttnParams& p, const Block& B, 
       const int c = chunk_key(kk);
       if (kk < len && R.has_rows && c <= R.w_hi_max && c + kChunkTokens > R.w_lo_min) {
         CopyOps ops(copy0 + copy_of(kk), lds_base + slot_of(kk), lane);
-        compute_rows<kF16Q>(R, L, c, ops, qb, qlo, scl, st);
+        compute_rows<kF16Q, true>(R, L, c, ops, qb, qlo, scl, st);
       }
     }
     if (k + 8 < len) pair_pages(p, B, Ld.bt0, chunk_key(k + 8), pp);
@@ -710,7 +713,15 @@ void attn_fwd_rows(const AttnParams p) {
     bf16x8 qb[2][4], qlo[2][4];
     if (R.has_rows) {
       load_q<kF16Q>(p, L[0], qb[0], qlo[0]);
-      if (R.two) load_q<kF16Q>(p, L[1], qb[1], qlo[1]);
+      if (R.two) {
+        load_q<kF16Q>(p, L[1], qb[1], qlo[1]);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          qb[1][j] = qb[0][j];
+          qlo[1][j] = qlo[0][j];
+        }
+      }
     }
     // Q has landed (a compiler-visible vmcnt(0): the chunk waits below are
     // asm the compiler does not see).
@@ -756,7 +767,7 @@ void attn_fwd_rows(const AttnParams p) {
       }
       if (mine) {
         Int8Ops ops{ch};
-        compute_rows<kF16Q>(R, L, c, ops, qb, qlo, scl, st);
+        compute_rows<kF16Q, false>(R, L, c, ops, qb, qlo, scl, st);
       }
     }
     const int ng = R.two ? 2 : 1;
