@@ -29,9 +29,10 @@
 // attn_kernel.cuh:540-600, softmax.cuh:91-170).
 //
 // Work order. Blocks are (request, token block, KV head), KV head fastest,
-// the token blocks of a request from its last (longest key range) to its
-// first; work-group b of W takes block b of each round of W blocks, in
-// reversed order on odd rounds, so long and short blocks pair up.
+// the requests of each group of 64 in decreasing order of estimated work, the
+// token blocks of a request from its last (longest key range) to its first;
+// work-group b of W takes block b of each round of W blocks, in reversed
+// order on odd rounds, so long and short blocks pair up.
 
 #include "attn_device.h"
 
@@ -84,12 +85,18 @@ __device__ __forceinline__ void make_block(const AttnParams& p, const RowTile& t
 }
 
 // The blocks of one work-group, in order (a prefix sum over requests, 64 per
-// wave instruction, as the unit table of attn_fwd.hip).
+// wave instruction, as the unit table of attn_fwd.hip). Within each group of
+// 64 requests the requests are taken in decreasing order of their estimated
+// work (row tiles x keys per row): the work-groups start on the long blocks
+// and the short ones fill the end, which evens out their finishing times
+// (a mixed prefill + decode batch whose long decodes came last left some
+// work-groups a decode block behind the others).
 template <bool kWindow>
 struct BlockWalk {
   int r0 = -64;
   int u0 = 0, u1 = 0;
   int incl = 0;
+  int sreq = 0;  // lane k: the request (within the group) of rank k
   int round = 0;
 
   __device__ __forceinline__ bool next(const AttnParams& p, int lane, Block& B) {
@@ -102,9 +109,23 @@ struct BlockWalk {
       u0 = u1;
       if (r0 >= p.num_reqs) return false;
       const int r = r0 + lane;
-      const int units = r < p.num_reqs
-                            ? request_row_tiles(p.qsl[r + 1] - p.qsl[r], p.blk_tok) * p.num_kv_heads
-                            : 0;
+      int tiles = 0;
+      float work = -1.0f;  // lanes past the last request sort last
+      if (r < p.num_reqs) {
+        const int q_len = p.qsl[r + 1] - p.qsl[r];
+        tiles = request_row_tiles(q_len, p.blk_tok);
+        work = static_cast<float>(tiles) *
+               static_cast<float>(p.seq_lens[r] - q_len / 2);
+      }
+      // Rank: requests with more work first, ties in request order.
+      int rank = 0;
+      for (int j = 0; j < 64; ++j) {
+        const float wj = __builtin_bit_cast(
+            float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, work), j));
+        rank += (wj > work || (wj == work && j < lane)) ? 1 : 0;
+      }
+      sreq = __builtin_amdgcn_ds_permute(rank * 4, lane);
+      const int units = __builtin_amdgcn_ds_permute(rank * 4, tiles * p.num_kv_heads);
       int x = units;
 #pragma unroll
       for (int dd = 1; dd < 64; dd <<= 1) {
@@ -116,7 +137,7 @@ struct BlockWalk {
     }
     const int local = u - u0;
     const int j = static_cast<int>(__popcll(__ballot(incl <= local)));
-    const int req = r0 + j;
+    const int req = r0 + __builtin_amdgcn_readlane(sreq, j);
     const int u_loc = local - (j > 0 ? __builtin_amdgcn_readlane(incl, j - 1) : 0);
     const int q_start = ld_ro(p.qsl, req);
     const int q_len = ld_ro(p.qsl, req + 1) - q_start;
