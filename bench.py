@@ -21,7 +21,7 @@ layer-call), and
 Warm-up: W untimed steps, continued until they add up to at least 0.3 s of
 GPU work (the step count run is printed as warmup_steps_run).
 
-Usage: python bench.py [--steps K] [--warmup W] [--config 1..5] [--no-cpu]
+Usage: python bench.py [--steps K] [--warmup W] [--config 1..5] [--query-tokens 1|4] [--no-cpu]
 """
 
 from __future__ import annotations
@@ -47,8 +47,10 @@ CELL = 264  # bytes per (token, KV head): K 128 + k_scale 4 + V 128 + v_scale 4
 # Untimed warm-up lasts at least this long (seconds of GPU work), W steps at least.
 WARMUP_MIN_S = 0.3
 
-def workload(config: int):
-    """(name, q_lens, seq_lens, Hq, Hkv, window, is_prefill) of a BASELINE config."""
+def workload(config: int, query_tokens: int = 1):
+    """(name, q_lens, seq_lens, Hq, Hkv, window, is_prefill) of a BASELINE config.
+    query_tokens: config 3's query tokens, 1 (plain decode) or 4 (MTP verify,
+    causal within the 4 drafted positions)."""
     import numpy as np
 
     if config == 1:
@@ -57,6 +59,10 @@ def workload(config: int):
         lens = [int(x) for x in np.random.default_rng(2024).integers(1024, 32768 + 1, 64)]
         return "cfg2-decode-64seq-32q8kv-L1k-32k", [1] * 64, lens, 32, 8, 0, False
     if config == 3:
+        if query_tokens == 4:
+            return "cfg3-verify4-1seq-L131072", [4], [131072], 32, 8, 0, False
+        if query_tokens != 1:
+            raise SystemExit("config 3 runs at 1 or 4 query tokens")
         return "cfg3-decode-1seq-L131072", [1], [131072], 32, 8, 0, False
     if config == 4:
         lens = [int(x) for x in np.random.default_rng(4044).integers(8192, 65536 + 1, 8)]
@@ -175,6 +181,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", type=int, default=2)
+    ap.add_argument("--query-tokens", type=int, default=1,
+                    help="config 3 only: 1 (decode) or 4 (MTP verify)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--copy-probe-mib", type=int, default=0,
@@ -205,7 +213,7 @@ def main() -> int:
         raise SystemExit("pth_flash_attn op library is not built (python pth-flash-attn_amd/build.py)")
     dev = "cuda:0"
     torch.cuda.set_device(0)
-    name, q_lens, seq_lens, Hq, Hkv, window, is_prefill = workload(a.config)
+    name, q_lens, seq_lens, Hq, Hkv, window, is_prefill = workload(a.config, a.query_tokens)
     G, D, BS = Hq // Hkv, 128, 16
     cache = build_cache(seq_lens, Hkv=Hkv, D=D, block_size=BS, seed=a.config, device=dev)
     q, qsl = make_queries(q_lens, Hq=Hq, D=D, seed=a.config + 100, device=dev)

@@ -29,6 +29,8 @@ def test_workloads_are_the_baseline_configs():
     assert len(L) == 64 and all(1024 <= x <= 32768 for x in L)
     name, q, L, Hq, Hkv, W, pf = bench.workload(3)
     assert (q, L, Hq, Hkv) == ([1], [131072], 32, 8)
+    name, q, L, Hq, Hkv, W, pf = bench.workload(3, 4)
+    assert (q, L, Hq, Hkv) == ([4], [131072], 32, 8) and "verify4" in name
     name, q, L, Hq, Hkv, W, pf = bench.workload(4)
     assert q == [16] * 8 and W == 2048 and all(8192 <= x <= 65536 for x in L)
     name, q, L, Hq, Hkv, W, pf = bench.workload(5)
