@@ -182,6 +182,13 @@ GRID_ROWS = [
     Case("rows-hnd", q_lens=[33, 1], seq_lens=[600, 90], layout="HND", seed=61),
     Case("rows-padded", q_lens=[20, 1], seq_lens=[20, 70], pad_tokens=7, seed=62),
     Case("rows-short", q_lens=[17, 1], seq_lens=[17, 1], seed=63),
+    # 100 requests: the block walk orders the requests of each group of 64 by
+    # their work (two groups here), with runs of equal work (ties broken by
+    # request index) and requests without query tokens.
+    Case("rows-many-requests",
+         q_lens=[40, 1, 0, 70] + [1] * 60 + [33] + [1] * 35,
+         seq_lens=[300, 500, 7, 70] + [200 + 40 * (i % 7) for i in range(60)] + [900]
+                  + [650] * 20 + [64 + 97 * i for i in range(15)], Hq=8, Hkv=2, seed=65),
 ]
 
 
