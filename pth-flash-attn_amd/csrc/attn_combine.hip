@@ -94,7 +94,7 @@ __device__ __forceinline__ int row_live_splits(const CombineParams& c, int r, in
   const int32_t n = tile_chunks(request_tile(r, q_start, q_len, seq_len, c.bq, j), c.window,
                                 c.causal != 0);
   int first, live;
-  stream_splits(at + static_cast<int64_t>(hu / kGroupUnits) * n, n, per, first, live);
+  stream_splits(at + static_cast<int64_t>(hu / c.gu) * n, n, per, first, live);
   return live;
 }
 

@@ -279,13 +279,18 @@ struct Work {
   __device__ __forceinline__ void init(const AttnParams& p, int lane) {
     const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
     if constexpr (kStream) {
+      // kGroupUnits / gu partition work-groups per work-group, interleaved:
+      // waves [v gu, (v + 1) gu) of work-group b are partition work-group
+      // v W + b (W work-groups), so a launch with little work still spreads
+      // its first partition work-groups over W compute units.
+      const int vpw = kGroupUnits / p.gu;
       d = StreamDesc{p.qsl, p.seq_lens, p.num_reqs, p.bq, kWindow ? p.window : 0,
-                     kWindow ? p.causal : 1, p.n_hg, static_cast<int32_t>(gridDim.x),
+                     kWindow ? p.causal : 1, p.n_hg, static_cast<int32_t>(gridDim.x) * vpw,
                      p.num_splits};
       int64_t total;
       per = stream_per(d, lane, total);
-      wg = blockIdx.x;
-      wave = w;
+      wg = (w / p.gu) * static_cast<int>(gridDim.x) + static_cast<int>(blockIdx.x);
+      wave = w % p.gu;
       pos = static_cast<int64_t>(wg) * per;
       stop = pos + per < total ? pos + per : total;
     } else {
@@ -308,7 +313,7 @@ struct Work {
         const int64_t end = sp.c0 + sp.n < stop ? sp.c0 + sp.n : stop;
         const int c1 = static_cast<int>(end - sp.c0);
         pos = end;
-        const int hu = sp.hg * kGroupUnits + wave;
+        const int hu = sp.hg * p.gu + wave;
         if (hu >= p.n_hu) continue;  // the group has fewer units than waves
         int first, live;
         stream_splits(sp.c0, sp.n, per, first, live);

@@ -42,6 +42,18 @@ constexpr int32_t kWaves = 4;
 // stream group, one per wave.
 constexpr int32_t kGroupUnits = 8;
 
+// KV-head units per stream group: the row tile's units rounded up to a power
+// of two, at most kGroupUnits. A work-group of kGroupUnits waves holds
+// kGroupUnits / group_units(n_hu) groups' worth of waves, and the split
+// partition counts that many partition work-groups per work-group, so a row
+// tile with fewer units than waves (few KV heads, a single row group) still
+// keeps every wave of the work-group streaming.
+PA_HD int32_t group_units(int32_t n_hu) {
+  int32_t g = 1;
+  while (g < n_hu && g < kGroupUnits) g <<= 1;
+  return g;
+}
+
 PA_HD uint32_t mulhi32(uint32_t a, uint32_t b) {
 #if defined(__HIP_DEVICE_COMPILE__)
   return __umulhi(a, b);

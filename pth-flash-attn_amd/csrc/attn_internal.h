@@ -53,7 +53,8 @@ struct AttnParams {
   Div32 rg_div;  // 16-row groups per row tile
   int32_t num_reqs;
   int32_t n_hu;  // KV-head units per row tile: num_kv_heads * row groups
-  int32_t n_hg;  // groups of kGroupUnits KV-head units: ceil(n_hu / 8)
+  int32_t gu;    // KV-head units per stream group: group_units(n_hu)
+  int32_t n_hg;  // stream groups per row tile: ceil(n_hu / gu)
   int32_t bq;    // query tokens per row tile
   int32_t group;
   int32_t num_splits;
@@ -95,8 +96,9 @@ struct CombineParams {
   int32_t bq;
   int32_t group;
   int32_t n_rg;
+  int32_t gu;      // KV-head units per stream group
   int32_t n_hg;
-  int32_t num_wg;
+  int32_t num_wg;  // partition work-groups: attention work-groups x kGroupUnits / gu
   int32_t window;
   int32_t causal;
   // A work-group per row (rows with many splits are merged by 4 waves)

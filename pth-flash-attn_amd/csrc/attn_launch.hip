@@ -112,8 +112,9 @@ void stream_fields(const PthAttnArgs& a, CombineParams& c) {
   c.bq = a.bq;
   c.group = group;
   c.n_rg = (rows + kRowsPerWave - 1) / kRowsPerWave;
-  c.n_hg = (a.num_kv_heads * c.n_rg + kGroupUnits - 1) / kGroupUnits;
-  c.num_wg = resident_workgroups();
+  c.gu = group_units(a.num_kv_heads * c.n_rg);
+  c.n_hg = (a.num_kv_heads * c.n_rg + c.gu - 1) / c.gu;
+  c.num_wg = resident_workgroups() * (kGroupUnits / c.gu);
   c.window = a.window;
   c.causal = a.causal;
 }
@@ -226,7 +227,8 @@ int32_t launch_attention(const PthAttnArgs& a, int32_t loader,
   p.rg_div = Div32::make(static_cast<uint32_t>(n_rg));
   p.num_reqs = a.num_reqs;
   p.n_hu = a.num_kv_heads * n_rg;
-  p.n_hg = (p.n_hu + kGroupUnits - 1) / kGroupUnits;
+  p.gu = group_units(p.n_hu);
+  p.n_hg = (p.n_hu + p.gu - 1) / p.gu;
   p.bq = a.bq;
   p.group = group;
   p.num_splits = a.num_splits;

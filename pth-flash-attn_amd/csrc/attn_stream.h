@@ -31,7 +31,7 @@ struct StreamDesc {
   int32_t bq;
   int32_t window;
   int32_t causal;
-  int32_t n_hg;      // groups of kGroupUnits KV-head units per row tile
+  int32_t n_hg;      // stream groups (of group_units(n_hu) KV-head units) per row tile
   int32_t num_wg;    // work-groups of the attention grid
   int32_t num_splits;
 };
