@@ -226,6 +226,17 @@ GRID_D = [
     Case("d256-bs7", q_lens=[3, 1], seq_lens=[100, 9], Hq=8, Hkv=2, D=256, block_size=7, seed=78),
     Case("d256-fp16q", q_lens=[1, 4], seq_lens=[300, 65], Hq=8, Hkv=2, D=256,
          q_dtype=torch.float16, seed=79),
+    # D = 256 on cell caches with pages of a multiple of 16 keys: the
+    # direct-to-LDS kernel with 256-byte swizzled key rows.
+    Case("d256-hnd", q_lens=[1, 4], seq_lens=[513, 90], Hq=12, Hkv=2, D=256, layout="HND",
+         seed=81),
+    Case("d256-bs64", q_lens=[1, 2, 1], seq_lens=[1000, 3333, 64], Hq=12, Hkv=2, D=256,
+         block_size=64, seed=82),
+    Case("d256-padded", q_lens=[1, 3], seq_lens=[50, 400], Hq=12, Hkv=2, D=256, pad_tokens=3,
+         seed=83),
+    Case("d256-long-ragged", q_lens=[1, 1, 1, 1, 2, 1], seq_lens=[131072, 7, 31, 33, 20000, 1],
+         Hq=12, Hkv=2, D=256, seed=84),
+    Case("d256-8kv", q_lens=[1, 3], seq_lens=[4000, 700], Hq=16, Hkv=8, D=256, seed=85),
 ]
 
 
