@@ -41,7 +41,6 @@ sys.path.insert(1, str(REPO))
 PEAK_HBM_GBS = 8000.0
 PEAK_BF16_TFLOPS = 2500.0
 METRIC = "µs/layer-call + achieved HBM GB/s (% peak), int8 paged decode D=128"
-CELL = 264  # bytes per (token, KV head): K 128 + k_scale 4 + V 128 + v_scale 4
 
 
 # Untimed warm-up lasts at least this long (seconds of GPU work), W steps at least.
@@ -76,27 +75,32 @@ def workload(config: int, query_tokens: int = 1):
     raise SystemExit(f"unknown config {config}")
 
 
-def visible_keys(q_lens, seq_lens, window):
+def visible_keys(q_lens, seq_lens, window, causal=True):
     """Per request: number of distinct keys any of its queries sees, and the
-    sum over its queries of visible keys (for flops)."""
+    sum over its queries of visible keys (for flops). Query i of a request
+    with q queries and L keys sits at p = L - q + i and sees [lo, hi]:
+    lo = p - W + 1 (W > 0) or 0; hi = p (causal), p + W - 1 (non-causal with
+    a window) or L - 1, clipped to [0, L - 1]."""
     union, pairs = [], 0
     for q, L in zip(q_lens, seq_lens):
-        lo_first = max(0, L - q - window + 1) if window > 0 else 0
-        union.append(L - lo_first)
+        first_lo, last_hi = L, -1
         for i in range(q):
             p = L - q + i
             lo = max(0, p - window + 1) if window > 0 else 0
-            pairs += p - lo + 1
+            hi = p if causal else (min(L - 1, p + window - 1) if window > 0 else L - 1)
+            first_lo, last_hi = min(first_lo, lo), max(last_hi, hi)
+            pairs += hi - lo + 1
+        union.append(max(0, last_hi - first_lo + 1))
     return union, pairs
 
 
-def algorithmic(q_lens, seq_lens, Hq, Hkv, window, block_size=16, D=128):
+def algorithmic(q_lens, seq_lens, Hq, Hkv, window, block_size=16, D=128, causal=True):
     """Bytes and flops one layer-call must move / do (reference crediting:
     Hkv (2D + 8) per visible key of each request, plus q, out and metadata;
     4 D Hq per visible query-key pair)."""
-    union, pairs = visible_keys(q_lens, seq_lens, window)
+    union, pairs = visible_keys(q_lens, seq_lens, window, causal)
     T = sum(q_lens)
-    kv = sum(union) * Hkv * CELL
+    kv = sum(union) * Hkv * (2 * D + 8)
     q_out = 2 * T * Hq * D * 2
     meta = sum(math.ceil(L / block_size) for L in seq_lens) * 4 + 4 * len(seq_lens) + 4 * (len(seq_lens) + 1)
     return kv + q_out + meta, kv + q_out // 2 + meta, 4 * D * Hq * pairs
@@ -175,6 +179,96 @@ def copy_ceiling(mib: int = 1024, reps: int = 10) -> dict:
             "frac_of_peak": round(gbs / PEAK_HBM_GBS, 4)}
 
 
+# The reference's published kernel rows closest to this path (its
+# docs/benchmarks.md:157-166, 190, 194; RTX 3080 20 GB at 220 W), each as
+# (q_lens, seq_lens, Hq, Hkv, D, block_size, window, causal, published us).
+# They are latency or small-bandwidth shapes on other hardware: context for a
+# user switching over, not the BASELINE metric.
+REFERENCE_ROWS = {
+    "drafter-16q4kv": ([8], [2056], 16, 4, 128, 864, 2048, False, 16.74),
+    "drafter-32q8kv": ([8], [2056], 32, 8, 128, 864, 2048, False, 24.16),
+    "drafter-16q4kv-L131080": ([8], [131080], 16, 4, 128, 864, 2048, False, 16.74),
+    "d256-decode-12q2kv-L128k": ([1], [131072], 12, 2, 256, 16, 0, True, 209.8),
+    "d256-verify4-12q2kv-L128k": ([4], [131072], 12, 2, 256, 16, 0, True, 247.2),
+}
+
+
+def reference_row(name: str, steps: int, warmup: int) -> dict:
+    """One of the reference's published rows through the op, steady state
+    (HIP events over `steps` layer calls after `warmup`)."""
+    import torch
+
+    from pth_flash_attn import ops, planner
+    from pth_flash_attn.cache import build_cache, make_queries
+
+    q_lens, seq_lens, Hq, Hkv, D, BS, window, causal, published = REFERENCE_ROWS[name]
+    dev = "cuda:0"
+    cache = build_cache(seq_lens, Hkv=Hkv, D=D, block_size=BS, seed=11, device=dev)
+    q, qsl = make_queries(q_lens, Hq=Hq, D=D, seed=12, device=dev)
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    q_max = max(q_lens)
+    ws_ts = planner.workspace_token_splits(max_num_seqs=len(q_lens), q_dec_max=q_max, Hkv=Hkv,
+                                           D=D, num_sms=cus)
+    plan = planner.plan_launch(num_tokens=len(q), num_reqs=len(q_lens), max_query_len=q_max,
+                               G=Hq // Hkv, Hkv=Hkv, D=D, num_sms=cus, is_prefill=False,
+                               ws_token_splits=max(ws_ts, len(q)), window=window)
+    S = plan.num_splits
+    out = torch.empty_like(q)
+    ws_o = torch.empty(plan.ws_o_shape if S > 1 else (0,), device=dev)
+    ws_lse = torch.empty(plan.ws_lse_shape if S > 1 else (0,), device=dev)
+
+    def step():
+        ops.pth_flash_attn_fwd(out, q, cache.k_cache, cache.v_cache, cache.k_scale,
+                               cache.v_scale, cache.block_table, cache.seq_lens, qsl, q_max,
+                               plan.wm, S, 1.0 / math.sqrt(D), ws_o, ws_lse, window, causal)
+
+    for _ in range(max(warmup, 200)):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) / steps * 1e3
+    # The same layer calls replayed from a captured graph (the reference times
+    # graph-replayed launches): no host launch work between the calls.
+    per_graph = 20
+    graph = torch.cuda.CUDAGraph()
+    cap = torch.cuda.Stream()
+    cap.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(cap):
+        step()
+        cap.synchronize()
+        with torch.cuda.graph(graph, stream=cap):
+            for _ in range(per_graph):
+                step()
+    torch.cuda.current_stream().wait_stream(cap)
+    for _ in range(5):
+        graph.replay()
+    torch.cuda.synchronize()
+    reps = max(steps // per_graph, 10)
+    e0.record()
+    for _ in range(reps):
+        graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    us_graph = e0.elapsed_time(e1) / (reps * per_graph) * 1e3
+    byts, _, _ = algorithmic(q_lens, seq_lens, Hq, Hkv, window, block_size=BS, D=D,
+                             causal=causal)
+    return {"metric": "us/layer-call, reference published row (warm)", "row": name,
+            "value": round(us, 2), "unit": "us", "higher_is_better": False, "steps": steps,
+            "us_graph_replay": round(us_graph, 2),
+            "reference_published_us": published, "reference_hardware": "RTX 3080 20 GB, 220 W",
+            "ratio_reference_over_ours": round(published / us, 2),
+            "ratio_reference_over_ours_graph": round(published / us_graph, 2),
+            "gbs": round(byts / us / 1e3, 1),
+            "config": {"q_lens": q_lens, "seq_lens": seq_lens, "Hq": Hq, "Hkv": Hkv, "D": D,
+                       "block_size": BS, "window": window, "causal": causal,
+                       "plan": {"wm": plan.wm, "num_splits": S}}}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -185,6 +279,8 @@ def main() -> int:
                     help="config 3 only: 1 (decode) or 4 (MTP verify)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-threads", type=int, default=0)
+    ap.add_argument("--reference-row", choices=sorted(REFERENCE_ROWS),
+                    help="time one of the reference's published rows instead of a config")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="only run a plain device copy of this many MiB, --steps times "
                          "(the reference point that scales rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -209,6 +305,12 @@ def main() -> int:
     from pth_flash_attn import capi, ops, planner
     from pth_flash_attn.cache import build_cache, make_queries
 
+    if a.reference_row:
+        if not ops.is_available():
+            raise SystemExit("pth_flash_attn op library is not built")
+        torch.cuda.set_device(0)
+        print(json.dumps(reference_row(a.reference_row, a.steps * 4, a.warmup)))
+        return 0
     if not ops.is_available():
         raise SystemExit("pth_flash_attn op library is not built (python pth-flash-attn_amd/build.py)")
     dev = "cuda:0"

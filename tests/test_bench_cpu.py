@@ -39,15 +39,17 @@ def test_workloads_are_the_baseline_configs():
     assert all(2048 <= x <= 65536 for x in L[4:])
 
 
-def _brute(q_lens, seq_lens, Hq, Hkv, window, D=128, block_size=16):
-    """Count visible keys one query at a time (bottom-right causal)."""
+def _brute(q_lens, seq_lens, Hq, Hkv, window, D=128, block_size=16, causal=True):
+    """Count visible keys one query at a time (bottom-right causal, or the
+    non-causal window [p - W + 1, p + W - 1] / every key)."""
     keys_seen, pairs = 0, 0
     for q, L in zip(q_lens, seq_lens):
         seen = set()
         for i in range(q):
             p = L - q + i
-            lo = max(0, p - window + 1) if window > 0 else 0
-            vis = range(lo, p + 1)
+            vis = [k for k in range(L)
+                   if (window == 0 or k > p - window)
+                   and (k <= p if causal else (window == 0 or k < p + window))]
             pairs += len(vis)
             seen.update(vis)
         keys_seen += len(seen)
@@ -70,6 +72,23 @@ def _brute(q_lens, seq_lens, Hq, Hkv, window, D=128, block_size=16):
 def test_algorithmic_work_matches_a_brute_force_count(q_lens, seq_lens, window):
     got = bench.algorithmic(q_lens, seq_lens, 32, 8, window)
     assert got == _brute(q_lens, seq_lens, 32, 8, window)
+
+
+@pytest.mark.parametrize("q_lens,seq_lens,window,D", [
+    ([8], [2056], 2048, 128),   # the reference's drafter rows: non-causal, window 2048
+    ([8], [300], 64, 128),
+    ([3, 5], [40, 700], 0, 256),
+])
+def test_algorithmic_work_non_causal_and_d256(q_lens, seq_lens, window, D):
+    got = bench.algorithmic(q_lens, seq_lens, 16, 4, window, D=D, causal=False)
+    assert got == _brute(q_lens, seq_lens, 16, 4, window, D=D, causal=False)
+
+
+def test_reference_rows_are_the_published_shapes():
+    row = bench.REFERENCE_ROWS["d256-decode-12q2kv-L128k"]
+    assert row[:6] == ([1], [131072], 12, 2, 256, 16) and row[-1] == 209.8
+    row = bench.REFERENCE_ROWS["drafter-32q8kv"]
+    assert row[:8] == ([8], [2056], 32, 8, 128, 864, 2048, False) and row[-1] == 24.16
 
 
 def test_config2_bytes_closed_form():
