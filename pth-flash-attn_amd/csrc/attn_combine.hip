@@ -321,12 +321,15 @@ __global__ __launch_bounds__(256) void combine_splits(const CombineParams c) {
 }
 
 // Few rows with many splits (shared_rows): a work-group of 16 waves per row;
-// wave w merges the 16-split blocks w, w + 16, ... (one round of loads for
-// up to 256 splits) and wave 0 merges the 16 results in a fixed order.
+// wave w merges the kBlk-split blocks w, w + 16, ... (one round of loads for
+// up to 16 kBlk splits) and wave 0 merges the 16 results in a fixed order.
+// kBlk is 16, or 32 for 257 to 512 splits (one block per wave: one
+// speculative round of LSE loads instead of a max pass and a pass per
+// block). Beyond 512 the workspace is an upper bound and a row's live splits
+// are often few, which 16-split blocks spread over more waves.
 constexpr int kSharedWaves = 16;
-constexpr int kSharedBlock = 16;
 
-template <int D>
+template <int D, int kSharedBlock>
 __global__ __launch_bounds__(kSharedWaves * 64) void combine_shared(const CombineParams c) {
   constexpr int NC = D / 64;
   __shared__ float part_m[kSharedWaves], part_den[kSharedWaves];
@@ -403,8 +406,11 @@ __global__ __launch_bounds__(256) void fill_unused_splits(const CombineParams c)
 
 template <int D>
 void launch_combine_d(const CombineParams& c, int64_t rows, hipStream_t stream) {
-  if (c.shared_rows)
-    hipLaunchKernelGGL(combine_shared<D>, dim3(static_cast<unsigned>(rows)),
+  if (c.shared_rows && c.num_splits > kSharedWaves * 16 && c.num_splits <= kSharedWaves * 32)
+    hipLaunchKernelGGL((combine_shared<D, 32>), dim3(static_cast<unsigned>(rows)),
+                       dim3(kSharedWaves * 64), 0, stream, c);
+  else if (c.shared_rows)
+    hipLaunchKernelGGL((combine_shared<D, 16>), dim3(static_cast<unsigned>(rows)),
                        dim3(kSharedWaves * 64), 0, stream, c);
   else
     hipLaunchKernelGGL(combine_splits<D>, dim3(static_cast<unsigned>((rows + kWaves - 1) / kWaves)),

@@ -252,6 +252,23 @@ def test_head_sizes_forced_splits(case, S):
     check_case(case, num_splits=S)
 
 
+# More than 256 splits on few rows: the shared combine with 32-split blocks
+# per wave (one speculative round of LSE loads for up to 512 splits).
+@pytest.mark.parametrize("case,S", [
+    (Case("many-splits-d256", q_lens=[1], seq_lens=[131072], Hq=12, Hkv=2, D=256, seed=86), 512),
+    (Case("many-splits-d128", q_lens=[1, 1], seq_lens=[65536, 3000], seed=87), 400),
+    (Case("many-splits-verify", q_lens=[4], seq_lens=[40000], seed=88), 300),
+], ids=lambda x: x.name if isinstance(x, Case) else str(x))
+def test_combine_many_splits(case, S):
+    check_case(case, num_splits=S)
+    # The op path: the combine reads each row's split count from the marker.
+    b = materialize(case, DEV)
+    out = run_op(b, num_splits=S)
+    ref_out, ref_lse, valid = oracle_of(b)
+    assert_parity(compare(out, None, ref_out, ref_lse, valid), name=case.name + "-op",
+                  strict=False)
+
+
 @pytest.mark.parametrize("D", [64, 256])
 def test_head_sizes_op_equals_capi(D):
     c = Case(f"op-d{D}", q_lens=[1, 4, 1], seq_lens=[3000, 400, 77], Hq=8, Hkv=2, D=D, seed=80)
