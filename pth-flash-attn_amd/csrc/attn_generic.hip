@@ -14,6 +14,8 @@
 
 #include "attn_device.h"
 
+// Build switch: 0 sends every D = 256 launch to the register-load kernel
+// (the comparison point of the direct-to-LDS D = 256 kernel below).
 #ifndef PA_PAGED256
 #define PA_PAGED256 1
 #endif
