@@ -236,6 +236,22 @@ int32_t pth_attn_attention_lse(const PthAttnArgs* args, float* lse,
  * the op's layer call. No counterpart in the reference's ABI. */
 int32_t pth_attn_attention_kernel(const PthAttnArgs* args, void* stream);
 
+/* pth_attn_attention_lse with no allocation and no workspace argument: the
+ * split partials live in a static device array of the library (64 MiB per
+ * GPU, held from the first call on a device until the process ends) instead
+ * of args->ws_o / args->ws_lse, which are ignored. lse may be NULL (then
+ * this is the op's layer call: attention + combine into args->out). Rejects
+ * with EINVAL, before any launch, a batch whose partials need more than the
+ * array: num_splits x num_tokens x num_q_heads x (head_size + 1) x 4 bytes
+ * (the ws_o part rounded up to 256) must be <= 64 MiB. Calls that overlap on
+ * one GPU (two streams, two threads) share the array and race; serialise
+ * them. No counterpart in the reference: it is for callers that cannot
+ * allocate (code under graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc). */
+int32_t pth_attn_attention_lse_noalloc(const PthAttnArgs* args, float* lse,
+                                       int64_t lse_stride_token,
+                                       int64_t lse_stride_head, void* stream);
+
 /* The int8 per-token-head cache writer: per (token, KV head), the fp32
  * absmax scale max(absmax / 127, 1e-6) and int8 = trunc(clamp(x * (1 /
  * scale) +- 0.5, -128, 127)), step for step as vLLM's writer (the reference's

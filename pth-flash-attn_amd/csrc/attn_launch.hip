@@ -10,6 +10,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <mutex>
 #include <string>
 
 #include "attn_internal.h"
@@ -409,6 +410,52 @@ PthAttnCombineArgs combine_of(const PthAttnArgs& a) {
   c.num_splits = a.num_splits;
   return c;
 }
+// Scratch of pth_attn_attention_lse_noalloc: the split partials (ws_o, then
+// ws_lse) of a launch live in this array instead of a caller's workspace.
+// Every GPU the library runs on holds its own copy until the process ends.
+// Host code never passes the array's name to a kernel (on the host it is a
+// stand-in, not a device address): each device's address is looked up once
+// with hipGetSymbolAddress, with that device current, and kept per device.
+// Nothing in it has to start at zero: a launch writes every partial slot and
+// split-count marker its combine reads before the combine runs.
+constexpr int64_t kScratchBytes = int64_t{64} << 20;
+static __device__ __attribute__((aligned(256))) char scratch[kScratchBytes];
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxScratchDevices] = {};
+
+// The current device's address of `scratch` (looked up on the first call on
+// that device).
+int32_t scratch_address(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return pa::fail(PTH_ATTN_ECUDA, std::string("hipGetDevice: ") + hipGetErrorString(e));
+  PA_REQUIRE(dev >= 0 && dev < kMaxScratchDevices,
+             "device ordinal " + std::to_string(dev) + " is beyond the scratch table");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr)
+      return pa::fail(PTH_ATTN_ECUDA, std::string("hipGetSymbolAddress(scratch): ") +
+                                          hipGetErrorString(e));
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return PTH_ATTN_OK;
+}
+
+// Bytes of the dense partial layout of `a` in the scratch: ws_o
+// [S, T, Hq, D] fp32 (256-byte aligned size), then ws_lse [S, T, Hq] fp32.
+int64_t scratch_o_bytes(const PthAttnArgs& a) {
+  const int64_t o = static_cast<int64_t>(a.num_splits) * a.num_tokens * a.num_q_heads *
+                    a.head_size * 4;
+  return (o + 255) / 256 * 256;
+}
+int64_t scratch_bytes(const PthAttnArgs& a) {
+  return scratch_o_bytes(a) + static_cast<int64_t>(a.num_splits) * a.num_tokens * a.num_q_heads * 4;
+}
 }  // namespace
 
 extern "C" {
@@ -485,6 +532,45 @@ int32_t pth_attn_attention_lse(const PthAttnArgs* args, float* lse,
   if (rc != PTH_ATTN_OK || args->num_splits == 1) return rc;
   return pa::launch_combine(combine_of(*args), st, lse, lse_stride_token, lse_stride_head,
                             args);
+}
+
+int32_t pth_attn_attention_lse_noalloc(const PthAttnArgs* args, float* lse,
+                                       int64_t lse_stride_token, int64_t lse_stride_head,
+                                       void* stream) {
+  pa::clear_error();
+  int32_t rc = check_args_abi(args);
+  if (rc != PTH_ATTN_OK) return rc;
+  PA_REQUIRE(args->out != nullptr, "out must be non-NULL");
+  PthAttnArgs a = *args;
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  if (a.num_splits > 1) {
+    PA_REQUIRE(a.num_tokens >= 1 && a.num_q_heads >= 1 &&
+                   (a.head_size == 64 || a.head_size == 128 || a.head_size == 256),
+               "num_tokens, num_q_heads and head_size must be valid to size the scratch");
+    const int64_t need = scratch_bytes(a);
+    PA_REQUIRE(need <= kScratchBytes,
+               "the split partials need " + std::to_string(need) +
+                   " bytes (num_splits x num_tokens x num_q_heads x (head_size + 1) x 4); "
+                   "the static scratch holds " + std::to_string(kScratchBytes) +
+                   " bytes: lower num_splits or split the batch");
+    void* base = nullptr;
+    rc = scratch_address(&base);
+    if (rc != PTH_ATTN_OK) return rc;
+    char* b = static_cast<char*>(base);
+    const int64_t hd = static_cast<int64_t>(a.head_size) * 4;
+    a.ws_o = reinterpret_cast<float*>(b);
+    a.ws_o_stride_head = hd;
+    a.ws_o_stride_token = hd * a.num_q_heads;
+    a.ws_o_stride_split = a.ws_o_stride_token * a.num_tokens;
+    a.ws_lse = reinterpret_cast<float*>(b + scratch_o_bytes(a));
+    a.ws_lse_stride_head = 4;
+    a.ws_lse_stride_token = 4 * static_cast<int64_t>(a.num_q_heads);
+    a.ws_lse_stride_split = a.ws_lse_stride_token * a.num_tokens;
+  }
+  rc = pa::launch_attention(a, 0, st, lse, lse_stride_token, lse_stride_head,
+                            /*fill_unused_splits=*/false);
+  if (rc != PTH_ATTN_OK || a.num_splits == 1) return rc;
+  return pa::launch_combine(combine_of(a), st, lse, lse_stride_token, lse_stride_head, &a);
 }
 
 }  // extern "C"

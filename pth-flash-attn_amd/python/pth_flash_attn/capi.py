@@ -35,6 +35,7 @@ EXPORTED_SYMBOLS = (
     "pth_attn_combine",
     "pth_attn_attention_lse",
     "pth_attn_attention_kernel",
+    "pth_attn_attention_lse_noalloc",
     "pth_attn_write_args_bytes",
     "pth_attn_write_kv",
 )
@@ -189,6 +190,9 @@ class AttnLib:
         lib.pth_attn_attention_lse.restype = i32
         lib.pth_attn_attention_lse.argtypes = [
             ctypes.POINTER(PthAttnArgs), vp, ctypes.c_int64, ctypes.c_int64, vp]
+        lib.pth_attn_attention_lse_noalloc.restype = i32
+        lib.pth_attn_attention_lse_noalloc.argtypes = [
+            ctypes.POINTER(PthAttnArgs), vp, ctypes.c_int64, ctypes.c_int64, vp]
         lib.pth_attn_write_kv.restype = i32
         lib.pth_attn_write_kv.argtypes = [ctypes.POINTER(PthAttnWriteArgs), vp]
         self.lib = lib
@@ -215,6 +219,16 @@ class AttnLib:
         """Run attention (+ combine) and write the natural-log LSE into `lse` [T, Hq] fp32."""
         es = lse.element_size()
         return self.lib.pth_attn_attention_lse(
+            ctypes.byref(args), lse.data_ptr(), lse.stride(0) * es, lse.stride(1) * es, stream)
+
+    def attention_lse_noalloc(self, args: PthAttnArgs, lse: Any = None,
+                              stream: int | None = None) -> int:
+        """attention_lse with the split partials in the library's static scratch
+        (args.ws_o / ws_lse ignored); lse may be None."""
+        if lse is None:
+            return self.lib.pth_attn_attention_lse_noalloc(ctypes.byref(args), None, 0, 0, stream)
+        es = lse.element_size()
+        return self.lib.pth_attn_attention_lse_noalloc(
             ctypes.byref(args), lse.data_ptr(), lse.stride(0) * es, lse.stride(1) * es, stream)
 
     def combine(self, args: PthAttnCombineArgs, stream: int | None = None) -> int:
