@@ -27,7 +27,7 @@ PY_PKG = PKG_ROOT / "python" / "pth_flash_attn"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
-HIP_SOURCES = ("attn_fwd.hip", "attn_rows.hip", "attn_generic.hip", "attn_combine.hip",
+HIP_SOURCES = ("attn_fwd.hip", "attn_staged.hip", "attn_rows.hip", "attn_generic.hip", "attn_combine.hip",
                "attn_launch.hip", "attn_writer.hip")
 # Packed fp32 VALU ops are disabled for all device code (they have given wrong
 # results on this pool); the host pass warns that it does not know the

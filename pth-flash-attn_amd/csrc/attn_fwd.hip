@@ -47,6 +47,12 @@
 
 #include "attn_device.h"
 
+#ifndef PA_REG_REALIGN
+#define PA_REG_REALIGN 0
+#endif
+#ifndef PA_DECODE_REG
+#define PA_DECODE_REG 0
+#endif
 #ifndef PA_PAGED_INFLIGHT
 #define PA_PAGED_INFLIGHT 1
 #endif
@@ -160,8 +166,11 @@ __device__ __forceinline__ void issue_chunk(const AttnParams& p, Prod& P, char* 
   if (P.k < P.U.n_chunks) producer_pages(p, P);
 }
 
+#ifndef PA_PAGED_WPE
+#define PA_PAGED_WPE 2
+#endif
 template <bool kWindow, bool kStream, bool kF16Q, int kInFlight>
-__global__ __launch_bounds__(kFwdWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
+__global__ __launch_bounds__(kFwdWaves * 64) __attribute__((amdgpu_waves_per_eu(PA_PAGED_WPE, PA_PAGED_WPE)))
 void attn_fwd_paged(const AttnParams p) {
   __shared__ __attribute__((aligned(16))) char lds_all[kFwdWaves * kInFlight * kSlotBytes];
   const int lane = threadIdx.x & 63;
@@ -367,12 +376,14 @@ void attn_fwd_paged_reg(const AttnParams p) {
           if (k + 2 < U.n_chunks) reg_pages(p, U, c + 2 * kChunkTokens, R);
         }
         compute_chunk<kF16Q>(U, L, c, ca, qb, qlo, scl, st);
+        if (PA_REG_REALIGN > 0 && (k % PA_REG_REALIGN) == PA_REG_REALIGN - 1) __builtin_amdgcn_s_barrier();
         if (++k >= U.n_chunks) break;
         if (k + 1 < U.n_chunks) {
           reg_load(p, R, lane, ca);
           if (k + 2 < U.n_chunks) reg_pages(p, U, c + 3 * kChunkTokens, R);
         }
         compute_chunk<kF16Q>(U, L, c + kChunkTokens, cb, qb, qlo, scl, st);
+        if (PA_REG_REALIGN > 0 && (k % PA_REG_REALIGN) == PA_REG_REALIGN - 1) __builtin_amdgcn_s_barrier();
         if (++k >= U.n_chunks) break;
       }
     }
@@ -388,9 +399,14 @@ constexpr int kPagedInFlight = PA_PAGED_INFLIGHT;
 // pipeline (the higher sustained bandwidth on long rows).
 constexpr int kShortWindow = 4096;
 
+#ifndef PA_USE_STAGED
+#define PA_USE_STAGED 1
+#endif
 template <bool W, bool St, bool F>
 hipError_t launch_paged(const AttnParams& p, dim3 grid, hipStream_t stream) {
-  if (W && p.window > 0 && p.window <= kShortWindow) {
+  if (PA_USE_STAGED && !(W && p.window > 0 && p.window <= kShortWindow))
+    return launch_staged_kernel(p, grid, W, F, stream);
+  if (PA_DECODE_REG || (W && p.window > 0 && p.window <= kShortWindow)) {
     hipLaunchKernelGGL((attn_fwd_paged_reg<W, St, F>), grid, dim3(kFwdWaves * 64), 0, stream, p);
   } else {
     hipLaunchKernelGGL((attn_fwd_paged<W, St, F, kPagedInFlight>), grid, dim3(kFwdWaves * 64), 0,

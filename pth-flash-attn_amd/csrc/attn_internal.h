@@ -69,6 +69,10 @@ struct AttnParams {
   int32_t blk_tok;
   int32_t num_kv_heads;
   float scale_log2;  // softmax_scale * log2(e)
+  // The page-row kernel applies (attn_staged.hip): the cell view is vLLM's
+  // NHD cell of 8 KV heads (264-byte cells, 2112-byte slot rows), pages of a
+  // multiple of 16 keys, and a work-group's 8 waves are the 8 KV heads.
+  int32_t page_rows;
 };
 
 struct CombineParams {
@@ -128,6 +132,8 @@ hipError_t launch_fwd_kernel(const AttnParams& p, dim3 grid, bool windowed,
                              bool paged16, bool q_f16, hipStream_t stream);
 // The register-load kernel for any block size and cache strides, head size
 // 64, 128 or 256 (attn_generic.hip); windowed / non-causal at 128 only.
+hipError_t launch_staged_kernel(const AttnParams& p, dim3 grid, bool windowed, bool q_f16,
+                                hipStream_t stream);
 hipError_t launch_generic_kernel(const AttnParams& p, dim3 grid, bool windowed, bool q_f16,
                                  int head_size, hipStream_t stream);
 // The row-block kernel (num_splits == 1, paged cell caches) and the query

@@ -240,6 +240,14 @@ int32_t launch_attention(const PthAttnArgs& a, int32_t loader,
   p.blk_tok = rows_block_tokens(group);
   p.num_kv_heads = a.num_kv_heads;
   p.scale_log2 = a.softmax_scale * kLog2e;
+  p.page_rows = 0;
+  if (p.cell && a.head_size == 128 && a.num_kv_heads == 8 && n_rg == 1 &&
+      a.block_size % 16 == 0 && p.cell_head == 264 && p.cell_slot == 8 * 264) {
+    bool inside = true;  // every stream of head h lies in bytes [264 h, 264 h + 264) of the row
+    for (int i = 0; i < 4; ++i)
+      inside = inside && p.cell_off[i] + (i < 2 ? 128u : 4u) <= 264u;
+    p.page_rows = inside ? 1 : 0;
+  }
 
   // Persistent grid. num_splits == 1: one wave per resident slot, but never
   // more waves than the unit table can hold (at most (T / bq + R) row tiles
