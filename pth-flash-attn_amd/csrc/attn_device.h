@@ -644,19 +644,6 @@ __device__ __forceinline__ bool writes_marker(const AttnParams& p, int s, int li
   return p.direct_single != 0 && p.num_splits > 1 && s == 0 && live < p.num_splits;
 }
 
-// Vector memory instructions store_finished issues for a unit, known before
-// it is issued (the lanes without a row are masked off, never the whole
-// wave: row 0 of a unit always exists), so that the waits of the chunk
-// pipeline can count past them.
-template <int D = 128>
-__device__ __forceinline__ int stores_per_unit(const AttnParams& p, int s, int live) {
-  constexpr int kCols = HeadDim<D>::kCols;
-  const int marker = writes_marker(p, s, live) ? 1 : 0;
-  if (!direct_out(p, live)) return kCols / 4 + 1 + marker;
-  return (p.out_dtype == PTH_ATTN_F32 ? kCols / 4 : kCols / 8) + (p.lse_out != nullptr ? 1 : 0) +
-         marker;
-}
-
 // Stores a finished unit: out (and lse_out, natural log) or its split's
 // partials. Split slots a row does not use are left untouched here
 // (fill_unused_splits writes them when a caller needs them).

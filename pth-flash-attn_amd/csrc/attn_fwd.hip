@@ -1,4 +1,7 @@
-// attn_fwd.hip -- the gfx950 paged int8 attention kernel, D = 128.
+// attn_fwd.hip -- the gfx950 paged int8 attention kernels, D = 128: the work
+// decomposition and MFMA layout they share, the register-load kernel for
+// short windows, and the dispatch between it and the register-staged
+// kernels of attn_staged.hip (long rows).
 //
 // Work decomposition. A work unit is (request, row tile, KV head, 16-row
 // group) over a range of keys; a row tile holds up to bq query tokens of one
@@ -47,247 +50,8 @@
 
 #include "attn_device.h"
 
-#ifndef PA_REG_REALIGN
-#define PA_REG_REALIGN 0
-#endif
-#ifndef PA_DECODE_REG
-#define PA_DECODE_REG 0
-#endif
-#ifndef PA_PAGED_INFLIGHT
-#define PA_PAGED_INFLIGHT 1
-#endif
-
 namespace pa {
 namespace {
-
-// ---------------------------------------------------------------------------
-// Paged kernel (block size a multiple of 16): the 16-key halves of a chunk
-// each lie in one page. A producer walks this wave's chunk sequence -- all
-// chunks of its units, in order -- and keeps the next PA_PAGED_INFLIGHT chunks
-// in flight in the wave's LDS slots with direct-to-LDS loads; the consumer
-// computes the chunk before them from registers. One slot is the default: the
-// consumer copies a chunk to registers, refills the slot and computes while
-// the next chunk loads. A second slot (two chunks in flight) measured 1-3 %
-// slower on the long-decode configurations: the deeper queue of DMA writes
-// into LDS costs more than the extra latency hiding buys. The producer crosses unit boundaries, so
-// a new unit's first chunks are already in flight while the previous unit
-// finishes: the pipeline does not drain between units.
-template <bool kWindow, bool kStream>
-struct Producer {
-  Work<kWindow, kStream> work;
-  Unit U;
-  int k;  // next chunk of U to issue
-  bool done;
-  // Cache pages and first slots of the two 16-key groups of chunk k, loaded
-  // one chunk ahead so that the issue never waits for the block table.
-  int32_t page[2];
-  int32_t slot0[2];
-  // Per-lane byte offsets within a 16-key group of one page (the cell view of
-  // the cache): K and V of two key rows (one per 8-key half), and one scale.
-  uint32_t off_k[2], off_v[2], off_s;
-};
-
-// The per-lane offsets of unit U's KV head.
-template <class Prod>
-__device__ __forceinline__ void producer_offsets(const AttnParams& p, Prod& P, int lane) {
-  const uint32_t kq = lane >> 3, piece = lane & 7;
-  const uint32_t head = static_cast<uint32_t>(P.U.kvh) * p.cell_head;
-  const uint32_t sw = 16u * (piece ^ kq);  // row r's piece c goes to LDS position c ^ (r & 7)
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const uint32_t row = (8u * h + kq) * p.cell_slot + head + sw;
-    P.off_k[h] = row + p.cell_off[0];
-    P.off_v[h] = row + p.cell_off[1];
-  }
-  P.off_s = static_cast<uint32_t>(lane & 15) * p.cell_slot + head +
-            (lane < 32 ? p.cell_off[2] : p.cell_off[3]);
-}
-
-// Block-table lookup for chunk k of the producer's unit (scalar loads; a
-// 16-key group outside the unit's keys reads page 0 and is masked later).
-template <class Prod>
-__device__ __forceinline__ void producer_pages(const AttnParams& p, Prod& P) {
-  const Unit& U = P.U;
-  const int c = U.c_begin + kChunkTokens * P.k;
-  const int64_t bt0 = static_cast<int64_t>(U.t.req) * p.bt_stride;
-#pragma unroll
-  for (int sub = 0; sub < 2; ++sub) {
-    const int c16 = c + 16 * sub;
-    P.page[sub] = 0;
-    P.slot0[sub] = 0;
-    if (c16 < U.ld_hi && c16 + 16 > U.ld_lo) {
-      const int blk = static_cast<int>(p.bs_div.div(c16));
-      P.slot0[sub] = c16 - blk * static_cast<int>(p.bs_div.d);
-      P.page[sub] = ld_ro(p.block_table, bt0 + blk);
-    }
-  }
-}
-
-// Moves the producer to its next chunk; false when the wave has no more.
-template <class Prod>
-__device__ __forceinline__ bool producer_next(const AttnParams& p, Prod& P, int lane) {
-  while (!P.done && P.k >= P.U.n_chunks) {
-    if (!P.work.next(p, lane, P.U)) {
-      P.done = true;
-      break;
-    }
-    P.k = 0;
-    if (P.U.n_chunks > 0) {
-      producer_offsets(p, P, lane);
-      producer_pages(p, P);
-    }
-  }
-  return !P.done;
-}
-
-// Issues the 9 direct-to-LDS loads of the producer's chunk k into `slot`:
-// 4 x 1 KB of K, 4 x 1 KB of V (8 keys x 128 bytes each) and the 64 scales,
-// then looks up the pages of chunk k + 1. Each 16-key group's address is a
-// uniform 64-bit base (page * page stride + first slot * slot stride, on the
-// scalar unit) plus the lane's 32-bit offset. Every address is inside the
-// cache: a key outside the unit's range reads another slot of the same page
-// (or of page 0) and is masked by the consumer, so every chunk issues
-// exactly kDmaPerChunk loads.
-template <class Prod>
-__device__ __forceinline__ void issue_chunk(const AttnParams& p, Prod& P, char* slot, int lane) {
-  const char* base[2];
-#pragma unroll
-  for (int sub = 0; sub < 2; ++sub)
-    base[sub] = p.cell_base +
-                static_cast<uint64_t>(static_cast<uint32_t>(P.page[sub])) * p.cell_block +
-                static_cast<uint32_t>(P.slot0[sub]) * p.cell_slot;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    dma16(base[i >> 1] + P.off_k[i & 1], slot + kSlotK + 1024 * i);
-    dma16(base[i >> 1] + P.off_v[i & 1], slot + kSlotV + 1024 * i);
-  }
-  dma4(((lane >> 4) & 1 ? base[1] : base[0]) + P.off_s, slot + kSlotScale);
-  ++P.k;
-  if (P.k < P.U.n_chunks) producer_pages(p, P);
-}
-
-#ifndef PA_PAGED_WPE
-#define PA_PAGED_WPE 2
-#endif
-template <bool kWindow, bool kStream, bool kF16Q, int kInFlight>
-__global__ __launch_bounds__(kFwdWaves * 64) __attribute__((amdgpu_waves_per_eu(PA_PAGED_WPE, PA_PAGED_WPE)))
-void attn_fwd_paged(const AttnParams p) {
-  __shared__ __attribute__((aligned(16))) char lds_all[kFwdWaves * kInFlight * kSlotBytes];
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  char* lds = lds_all + wave * kInFlight * kSlotBytes;
-  const uint32_t lds_base = lds_offset(lds);
-  const ReadOffsets ro = read_offsets(lane);
-  const float scl = scale_factor(lane & 15, p.scale_log2);
-
-  Producer<kWindow, kStream> P;
-  P.work.init(p, lane);
-  P.U.n_chunks = 0;
-  P.k = 0;
-  P.done = false;
-  Work<kWindow, kStream> work = P.work;  // the consumer's walk: the same units, behind
-  Unit U;
-  Lanes L;
-  State st;
-  bf16x8 qb[4], qlo[4];
-  int ck = 0;
-  bool have = false;
-  int slot_r = 0;
-  // The consumer's first unit is located, and its query load issued, before
-  // the producer's first chunk: the two loads are in flight together (a
-  // short launch is a chain of dependent loads per wave).
-  while (work.next(p, lane, U)) {
-    if (!U.has_rows) continue;
-    L = unit_lanes<kWindow>(p, U, lane);
-    if (U.n_chunks == 0) {  // no key of these rows in this split
-      State empty;
-      state_reset(empty);
-      epilogue(p, U, L, empty);
-      continue;
-    }
-    have = true;
-    break;
-  }
-  if (have) load_q<kF16Q>(p, L, qb, qlo);
-
-  int inflight = 0;  // chunks issued and not yet consumed
-  int slot_w = 0;    // slot the producer fills next
-#pragma unroll
-  for (int i = 0; i < kInFlight; ++i) {
-    if (producer_next(p, P, lane)) {
-      issue_chunk(p, P, lds + slot_w * kSlotBytes, lane);
-      ++inflight;
-      slot_w = slot_w + 1 == kInFlight ? 0 : slot_w + 1;
-    }
-  }
-  // Compiler-visible wait for the query (it also waits for the chunks just
-  // issued, which the first step needs anyway).
-  __builtin_amdgcn_s_waitcnt(0x0F70);
-  state_reset(st);
-  // The stores of a finished unit are issued after the wait that drains the
-  // pipeline at the unit switch: vector memory operations complete in issue
-  // order, so a store issued in front of chunks still in flight would make
-  // every wait for those chunks wait for the store as well. The waits of
-  // the chunks that were in flight before the stores count past them.
-  int n_store = 0;
-  int older_than_stores = 0;  // chunks in flight issued before the last stores
-  while (true) {
-    if (!have || ck >= U.n_chunks) {
-      Finished done;
-      const bool had = have;
-      if (have) finish(U, L, st, done);
-      have = false;
-      while (work.next(p, lane, U)) {
-        if (!U.has_rows) continue;
-        L = unit_lanes<kWindow>(p, U, lane);
-        if (U.n_chunks == 0) {  // no key of these rows in this split
-          State empty;
-          state_reset(empty);
-          epilogue(p, U, L, empty);
-          continue;
-        }
-        have = true;
-        break;
-      }
-      if (have) load_q<kF16Q>(p, L, qb, qlo);
-      // A compiler-visible wait for Q here (vmcnt(0): it also drains this
-      // unit's chunks in flight, once per unit) keeps the compiler from
-      // re-waiting for Q, with vmcnt(0), before every chunk of the loop.
-      __builtin_amdgcn_s_waitcnt(0x0F70);
-      if (had) {
-        store_finished(p, done);
-        n_store = stores_per_unit(p, done.s, done.live);
-        older_than_stores = inflight;
-      }
-      if (!have) break;
-      state_reset(st);
-      ck = 0;
-    }
-    // Operations issued after the chunk about to be read: the next chunk's
-    // loads when it is in flight, and the last unit's stores when they were
-    // issued after this chunk's loads.
-    wait_vmcnt_dyn((kInFlight >= 2 && inflight >= 2 ? kDmaPerChunk : 0) +
-                   (older_than_stores > 0 ? n_store : 0));
-    if (older_than_stores > 0) --older_than_stores;
-    Chunk ch;
-    read_chunk(lds_base + slot_r * kSlotBytes, ro, ch);  // returns once the reads landed
-    --inflight;
-    slot_r = slot_r + 1 == kInFlight ? 0 : slot_r + 1;
-    if (producer_next(p, P, lane)) {
-      issue_chunk(p, P, lds + slot_w * kSlotBytes, lane);
-      ++inflight;
-      slot_w = slot_w + 1 == kInFlight ? 0 : slot_w + 1;
-    }
-    compute_chunk<kF16Q>(U, L, U.c_begin + kChunkTokens * ck, ch, qb, qlo, scl, st);
-    // Re-align the work-group's waves now and then: they read adjacent cells
-    // whose shared cache lines are fetched once only while the waves stay
-    // close (a wave running far ahead gets them evicted before its
-    // neighbour asks). Only a rendezvous: no data passes through it, and a
-    // wave that has finished its work no longer holds the others.
-    if ((ck & (kRealignChunks - 1)) == kRealignChunks - 1) __builtin_amdgcn_s_barrier();
-    ++ck;
-  }
-}
 
 // ---------------------------------------------------------------------------
 // Paged kernel with register loads (block size a multiple of 16, cell view of
@@ -376,14 +140,12 @@ void attn_fwd_paged_reg(const AttnParams p) {
           if (k + 2 < U.n_chunks) reg_pages(p, U, c + 2 * kChunkTokens, R);
         }
         compute_chunk<kF16Q>(U, L, c, ca, qb, qlo, scl, st);
-        if (PA_REG_REALIGN > 0 && (k % PA_REG_REALIGN) == PA_REG_REALIGN - 1) __builtin_amdgcn_s_barrier();
         if (++k >= U.n_chunks) break;
         if (k + 1 < U.n_chunks) {
           reg_load(p, R, lane, ca);
           if (k + 2 < U.n_chunks) reg_pages(p, U, c + 3 * kChunkTokens, R);
         }
         compute_chunk<kF16Q>(U, L, c + kChunkTokens, cb, qb, qlo, scl, st);
-        if (PA_REG_REALIGN > 0 && (k % PA_REG_REALIGN) == PA_REG_REALIGN - 1) __builtin_amdgcn_s_barrier();
         if (++k >= U.n_chunks) break;
       }
     }
@@ -391,28 +153,18 @@ void attn_fwd_paged_reg(const AttnParams p) {
   }
 }
 
-// Chunks in flight per wave on the paged path (LDS slots per wave).
-constexpr int kPagedInFlight = PA_PAGED_INFLIGHT;
-
 // Windows up to this many keys: the register-load kernel (its short
-// latency wins when every row reads few keys); otherwise the direct-to-LDS
-// pipeline (the higher sustained bandwidth on long rows).
+// latency wins when every row reads few keys); otherwise the register-staged
+// kernels of attn_staged.hip (the higher sustained bandwidth on long rows).
 constexpr int kShortWindow = 4096;
 
-#ifndef PA_USE_STAGED
-#define PA_USE_STAGED 1
-#endif
 template <bool W, bool St, bool F>
 hipError_t launch_paged(const AttnParams& p, dim3 grid, hipStream_t stream) {
-  if (PA_USE_STAGED && !(W && p.window > 0 && p.window <= kShortWindow))
-    return launch_staged_kernel(p, grid, W, F, stream);
-  if (PA_DECODE_REG || (W && p.window > 0 && p.window <= kShortWindow)) {
+  if (W && p.window > 0 && p.window <= kShortWindow) {
     hipLaunchKernelGGL((attn_fwd_paged_reg<W, St, F>), grid, dim3(kFwdWaves * 64), 0, stream, p);
-  } else {
-    hipLaunchKernelGGL((attn_fwd_paged<W, St, F, kPagedInFlight>), grid, dim3(kFwdWaves * 64), 0,
-                       stream, p);
+    return hipGetLastError();
   }
-  return hipGetLastError();
+  return launch_staged_kernel(p, grid, W, F, stream);
 }
 template <bool W, bool St>
 hipError_t launch_variant(const AttnParams& p, dim3 grid, bool q_f16, hipStream_t stream) {

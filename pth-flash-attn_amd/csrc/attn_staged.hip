@@ -1,36 +1,30 @@
-// attn_staged.hip -- the paged attention kernel with register-staged loads
-// (block size a multiple of 16, cell view of the cache, D = 128).
+// attn_staged.hip -- the paged attention kernels with register-staged loads
+// (block size a multiple of 16, cell view of the cache, D = 128): the
+// long-row decode, verify and split path.
 //
-// Same work decomposition, MFMA layout and numerics as attn_fwd_paged
-// (attn_fwd.hip); only the way a 32-key chunk reaches LDS differs. Each wave
-// loads its KV head's cells of the next chunk with ordinary 16-byte vector
-// loads in "row" order: lane (t, c) = (lane / 8, lane % 8) reads piece c of
-// key row t of an 8-key group, so one instruction covers 8 whole 128-byte
-// rows. The chunk waits in 33 VGPRs while the current chunk is computed out
-// of the wave's LDS slot; once the computation is done the wave writes the
-// staged chunk into the slot (in the swizzled layout the MFMA operand reads
-// expect) and immediately issues the loads of the chunk after it. So every
-// wave keeps exactly one chunk in flight, the compute of the previous chunk
-// overlapped, and the gap between two chunks' loads is only the slot write.
+// Same work decomposition, MFMA layout and numerics as attn_fwd.hip; what
+// differs is how a 32-key chunk reaches LDS. Loads are ordinary 16-byte
+// vector loads into registers, issued as soon as the previous chunk has been
+// moved from registers into LDS, so each wave keeps one chunk in flight while
+// it computes the chunk before it out of LDS. Two kernels:
 //
-// Why not direct-to-LDS loads: measured on MI355X with the cell layout of
-// config 2 (8 KV heads, pages of 16 keys, shuffled pages, 2.2 GB), a read
-// loop with direct-to-LDS loads and one 32-key chunk in flight per wave
-// reaches 5.2 TB/s; the same bytes by register loads in row order, written
-// to LDS and read back, 6.0 TB/s; two chunks in flight per wave are slower
-// with either kind of load.
+//  * attn_fwd_pagerows (the vLLM NHD cell of 8 KV heads, work-groups whose
+//    8 waves are the 8 heads of the same keys): the work-group loads whole
+//    slot rows (every cache line by exactly one wave) into a shared LDS
+//    chunk buffer, one barrier per chunk;
+//  * attn_fwd_staged (any other cell cache): each wave loads its own head's
+//    cells in row order (lane (t, c) reads 16-byte piece c of key t, so one
+//    instruction covers 8 whole 128-byte rows) into its own LDS slot.
+//
+// Measured on MI355X with config 2's cache (8 KV heads, pages of 16 keys,
+// shuffled pages, 2.2 GB) in a read-only loop: direct-to-LDS loads with one
+// 32-key chunk in flight per wave reach 5.2 TB/s, the register-staged row
+// loads 6.0 TB/s; two chunks in flight per wave are slower with either.
+// The page-row kernel runs config 2 at 364 us (the per-wave staged kernel
+// 396 us: its waves read cache lines shared with the neighbouring head and
+// re-fetch them when they drift apart).
 
 #include "attn_device.h"
-
-#ifndef PA_STAGED_XUNIT
-#define PA_STAGED_XUNIT 0
-#endif
-#ifndef PA_STAGED_RO_REG
-#define PA_STAGED_RO_REG 1
-#endif
-#ifndef PA_STAGED_REALIGN
-#define PA_STAGED_REALIGN 8
-#endif
 
 namespace pa {
 namespace {
@@ -79,11 +73,7 @@ __device__ __forceinline__ ChunkPages chunk_pages(const AttnParams& p, const Uni
     if (c16 < U.ld_hi && c16 + 16 > U.ld_lo) {
       const int blk = static_cast<int>(p.bs_div.div(c16));
       cp.slot0[sub] = c16 - blk * static_cast<int>(p.bs_div.d);
-#ifdef PA_STAGED_FAKEPAGES
-      cp.page[sub] = static_cast<int32_t>((static_cast<uint32_t>(bt0 + blk) * 2654435761u) % 60000u);
-#else
       cp.page[sub] = ld_ro(p.block_table, bt0 + blk);
-#endif
     }
   }
   return cp;
@@ -190,84 +180,11 @@ void attn_fwd_staged(const AttnParams p) {
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   char* slot = lds_all + wave * kSlotBytes;
-#if PA_STAGED_RO_REG
   const ReadOffsets ro = read_offsets(lane);
-#define PA_RO ro
-#else
-#define PA_RO read_offsets(lane)
-#endif
   const float scl = scale_factor(lane & 15, p.scale_log2);
 
-#ifdef PA_STAGED_TIMES
-  const uint64_t t_start = __builtin_amdgcn_s_memrealtime();
-#endif
   Work<kWindow, kStream> work;
   work.init(p, lane);
-#if PA_STAGED_XUNIT
-  Unit U;
-  Lanes L;
-  int realign = 0;
-  if (next_live_unit(p, work, lane, U, L)) {
-  // The unit being computed (U, L, so, qb) and, during its last chunk, the
-  // next unit, whose first chunk and query are then already in flight: the
-  // pipeline does not drain between units.
-  StageOffsets so = stage_offsets(p, U.kvh, lane);
-  Staged S;
-  ChunkPages cp = chunk_pages(p, U, U.c_begin);
-  stage_load(p, cp, so, lane, S);
-  bf16x8 qb[4], qlo[4];
-  load_q<kF16Q>(p, L, qb, qlo);
-  if (U.n_chunks > 1) cp = chunk_pages(p, U, U.c_begin + kChunkTokens);
-  while (true) {
-    State st;
-    state_reset(st);
-    Unit Un;
-    Lanes Ln;
-    StageOffsets son;
-    bf16x8 qbn[4], qlon[4];
-    bool have_next = false;
-    for (int k = 0; k < U.n_chunks; ++k) {
-      // Chunk k is in S: move it to the slot, start the next chunk (of this
-      // unit or, after its last, of the next unit), then compute chunk k
-      // from the slot.
-      stage_write(slot, lane, S);
-      if (k + 1 < U.n_chunks) {
-        stage_load(p, cp, so, lane, S);
-        if (k + 2 < U.n_chunks) cp = chunk_pages(p, U, U.c_begin + kChunkTokens * (k + 2));
-      } else {
-        have_next = next_live_unit(p, work, lane, Un, Ln);
-        if (have_next) {
-          son = stage_offsets(p, Un.kvh, lane);
-          cp = chunk_pages(p, Un, Un.c_begin);
-          stage_load(p, cp, son, lane, S);
-          load_q<kF16Q>(p, Ln, qbn, qlon);
-          if (Un.n_chunks > 1) cp = chunk_pages(p, Un, Un.c_begin + kChunkTokens);
-        }
-      }
-      Chunk ch;
-      slot_read(slot, PA_RO, ch);
-      compute_chunk<kF16Q>(U, L, U.c_begin + kChunkTokens * k, ch, qb, qlo, scl, st);
-      // Re-align the work-group's waves now and then (they read adjacent
-      // cells whose shared cache lines are fetched once while the waves stay
-      // close). A wave that has finished no longer holds the others.
-      if (PA_STAGED_REALIGN > 0 && ++realign == PA_STAGED_REALIGN) {
-        realign = 0;
-        __builtin_amdgcn_s_barrier();
-      }
-    }
-    epilogue(p, U, L, st);
-    if (!have_next) break;
-    U = Un;
-    L = Ln;
-    so = son;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      qb[j] = qbn[j];
-      qlo[j] = qlon[j];
-    }
-  }
-  }
-#else
   Unit U;
   Lanes L;
   int realign = 0;
@@ -290,34 +207,18 @@ void attn_fwd_staged(const AttnParams p) {
         if (k + 2 < U.n_chunks) cp = chunk_pages(p, U, U.c_begin + kChunkTokens * (k + 2));
       }
       Chunk ch;
-      slot_read(slot, PA_RO, ch);
-#ifdef PA_STAGED_NOCOMP
-      // Timing experiment only: no arithmetic (wrong results).
-      st.o[0][0] += __builtin_bit_cast(float, ch.k[0][0][0] ^ ch.k[1][1][3] ^ ch.v[0][0] ^ ch.v[7][1]) + ch.sc;
-#else
+      slot_read(slot, ro, ch);
       compute_chunk<kF16Q>(U, L, U.c_begin + kChunkTokens * k, ch, qb, qlo, scl, st);
-#endif
       // Re-align the work-group's waves now and then (they read adjacent
       // cells whose shared cache lines are fetched once while the waves stay
       // close). A wave that has finished no longer holds the others.
-      if (PA_STAGED_REALIGN > 0 && ++realign == PA_STAGED_REALIGN) {
+      if (++realign == kRealignChunks) {
         realign = 0;
         __builtin_amdgcn_s_barrier();
       }
     }
     epilogue(p, U, L, st);
   }
-#endif
-#ifdef PA_STAGED_TIMES
-  // Debug timing: start and end of each wave in the last split slot of ws_o.
-  if (lane == 0 && p.num_splits > 1) {
-    uint64_t* t = reinterpret_cast<uint64_t*>(reinterpret_cast<char*>(p.ws_o) +
-                                              (p.num_splits - 1) * p.s_wo_split) +
-                  2 * (blockIdx.x * kFwdWaves + wave);
-    t[0] = t_start;
-    t[1] = __builtin_amdgcn_s_memrealtime();
-  }
-#endif
 }
 
 
