@@ -1,27 +1,41 @@
 #!/usr/bin/env python3
-"""Benchmark of the hot path: int8 paged decode attention, D = 128, on one MI355X.
+"""Benchmark of the hot path: int8 paged attention, D = 128, on one MI355X.
 
-Default workload ("config 2"): 64 decode sequences, 1 query
-token each, 32 q / 8 KV heads, D = 128, context lengths uniform in [1k, 32k]
-(seeded), vLLM block size 16 with a shuffled block table over one shared pool,
-int8 K/V with inline fp32 per-token-head scales, bf16 queries ~ N(0, 1).
-A step is one layer-call: the torch op pth_flash_attn_fwd (attention kernel +
-split combine) with the planner's plan, inputs resident in HBM.
+Headline workload ("config 2"): 64 decode sequences, 1
+query token each, 32 q / 8 KV heads, D = 128, context lengths uniform in
+[1k, 32k] (seeded), vLLM block size 16 with a shuffled block table over one
+shared pool, int8 K/V with inline fp32 per-token-head scales, bf16 queries
+~ N(0, 1). A step is one layer call: the torch op pth_flash_attn_fwd
+(attention kernel + split combine) with the planner's plan, inputs resident
+in HBM.
 
-Printed (one JSON line on stdout): value = achieved HBM GB/s of the whole
-layer-call (algorithmic bytes / time), ms_per_step (x1000 = us per
-layer-call), and
-  roofline     - the attention kernel alone: algorithmic bytes of one launch /
-                 its average duration (HIP events on the launch stream), against
-                 MI355X's 8 TB/s, with HBM traffic per launch from rocprofv3
-                 counters when a profile summary is present (else null);
-  cpu_baseline - the repository's CPU oracle (fp64 restatement of the
-                 reference's CPU path) on a bounded sample of the same workload.
+Printed (one JSON line on stdout):
+  value / ms_per_step  the headline layer call: algorithmic bytes / time over
+                       exactly K eager steps after W warm-up steps (HIP events
+                       on the launch stream, synchronised on both sides);
+  roofline             the attention kernel alone (HIP events over K launches
+                       on the launch stream), its algorithmic bytes per launch
+                       against MI355X's 8 TB/s, the HBM traffic per launch from
+                       the committed rocprofv3 counter summary (or null), and
+                       the measured read ceiling of the same bytes;
+  configs              every BASELINE configuration (1, 2, 3 at 1 and 4 query
+                       tokens, 4, 5): layer call (eager mean and the median of
+                       graph-replayed calls), attention and combine kernels
+                       timed alone, GB/s or TFLOP/s against the roofline, and
+                       the CPU baseline. Inputs smaller than 1 GiB are rotated
+                       over copies so that at least 1 GiB passes between two
+                       reads of the same bytes (cold MALL);
+  read_ceiling         bench_hip/ceilings.hip: config 2's exact cache bytes read
+                       with the attention kernel's load pattern and discarded;
+  mfma_ceiling         bench_hip/ceilings.hip: dense bf16 MFMA rate at 8 waves
+                       per CU;
+  cpu_baseline         the repository's CPU oracle (fp64 restatement of the
+                       reference's CPU path) on a bounded sample of the
+                       headline workload, on the host cores (threads used and
+                       the host's CPU count stated).
 
-Warm-up: W untimed steps, continued until they add up to at least 0.3 s of
-GPU work (the step count run is printed as warmup_steps_run).
-
-Usage: python bench.py [--steps K] [--warmup W] [--config 1..5] [--query-tokens 1|4] [--no-cpu]
+Usage: python bench.py [--steps K] [--warmup W] [--config 1..5] [--query-tokens 1|4]
+                       [--no-cpu] [--only-headline]
 """
 
 from __future__ import annotations
@@ -106,8 +120,13 @@ def algorithmic(q_lens, seq_lens, Hq, Hkv, window, block_size=16, D=128, causal=
     return kv + q_out + meta, kv + q_out // 2 + meta, 4 * D * Hq * pairs
 
 
-def cpu_baseline(cache, q, qsl, q_lens, seq_lens, Hq, Hkv, window, threads):
-    """Time the CPU oracle on a bounded sample (about 10 s) of the workload."""
+def cpu_baseline(cache, q, qsl, q_lens, seq_lens, Hq, Hkv, window, threads,
+                 budget_s: float = 4.0) -> dict:
+    """Time the CPU oracle on a bounded sample of the workload (about
+    budget_s of CPU work): whole requests from the first on, or for a batch
+    whose first request is a long prefill chunk, its first query tokens.
+    The rate is in the workload's unit: GB/s of credited bytes, or TFLOP/s
+    of credited flops for a batch with prefill chunks."""
     import torch
 
     import oracle
@@ -121,6 +140,27 @@ def cpu_baseline(cache, q, qsl, q_lens, seq_lens, Hq, Hkv, window, threads):
                           block_table=host.block_table, seq_lens=host.seq_lens,
                           query_start_loc=qslh, bq=1, num_splits=1,
                           softmax_scale=1.0 / math.sqrt(128), window=window)
+    prefill = max(q_lens) > 64
+    total_bytes, _, total_flops = algorithmic(q_lens, seq_lens, Hq, Hkv, window)
+    if prefill:
+        # Query tokens [0, n) of the first request (a prefill chunk).
+        n, elapsed = 16, 0.0
+        while True:
+            n = min(n, q_lens[0])
+            t0 = time.perf_counter()
+            oracle.attention(args, threads=threads, rows=(0, n))
+            elapsed = time.perf_counter() - t0
+            if elapsed > budget_s or n == q_lens[0]:
+                break
+            n = max(n * 2, int(n * 2.0 * budget_s / max(elapsed, 1e-3)))
+        L, ql = seq_lens[0], q_lens[0]
+        pairs = sum(min(L - ql + i, L - 1) + 1 for i in range(n))  # causal, no window
+        flops = 4 * 128 * Hq * pairs
+        return {"value": round(flops / elapsed / 1e12, 4), "unit": "TFLOP/s", "cores": threads,
+                "host_cpus": os.cpu_count(), "kind": "port",
+                "sample": f"query tokens [0, {n}) of the first 2048-token prefill chunk, "
+                          f"{elapsed:.2f} s, fp64 oracle/oracle.c",
+                "us_per_layer_call_extrapolated": round(elapsed * 1e6 * total_flops / flops, 1)}
     starts = [0]
     for ql in q_lens:
         starts.append(starts[-1] + ql)
@@ -131,16 +171,15 @@ def cpu_baseline(cache, q, qsl, q_lens, seq_lens, Hq, Hkv, window, threads):
         oracle.attention(args, threads=threads, rows=(0, starts[n_req]))
         elapsed = time.perf_counter() - t0
         done = n_req
-        if elapsed > 4.0 or n_req == len(q_lens):
+        if elapsed > budget_s or n_req == len(q_lens):
             break
-        n = max(n * 2, int(n * 8.0 / max(elapsed, 1e-3)))
-    byts, _, flops = algorithmic(q_lens[:done], seq_lens[:done], Hq, Hkv, window)
+        n = max(n * 2, int(n * 2.0 * budget_s / max(elapsed, 1e-3)))
+    byts, _, _ = algorithmic(q_lens[:done], seq_lens[:done], Hq, Hkv, window)
     return {"value": round(byts / elapsed / 1e9, 3), "unit": "GB/s", "cores": threads,
-            "kind": "port",
+            "host_cpus": os.cpu_count(), "kind": "port",
             "sample": f"first {done} of {len(q_lens)} requests ({sum(q_lens[:done])} query tokens), "
                       f"{elapsed:.2f} s, fp64 oracle/oracle.c",
-            "us_per_layer_call_extrapolated": round(
-                elapsed * 1e6 * algorithmic(q_lens, seq_lens, Hq, Hkv, window)[0] / byts, 1)}
+            "us_per_layer_call_extrapolated": round(elapsed * 1e6 * total_bytes / byts, 1)}
 
 
 def profile_traffic(kernel_prefix: str, workload_name: str):
@@ -156,27 +195,64 @@ def profile_traffic(kernel_prefix: str, workload_name: str):
         return None
 
 
-def copy_ceiling(mib: int = 1024, reps: int = 10) -> dict:
-    """Achievable streaming HBM throughput on this device, for context next to
-    the nominal peak: a plain device copy of ``mib`` MiB (read + write bytes
-    over its time, HIP events). Measured: ~6.1-6.2 TB/s also for pure reads
-    of the paged cache, by any access pattern."""
+def bench_lib():
+    """bench_hip/libpth_bench.so (the measured ceilings), loaded with ctypes."""
+    import ctypes
+
+    path = REPO / "bench_hip" / "libpth_bench.so"
+    if not path.is_file():
+        raise SystemExit(f"{path} is not built (python bench_hip/build.py)")
+    lib = ctypes.CDLL(str(path))
+    f32, i32, i64, vp = ctypes.c_float, ctypes.c_int32, ctypes.c_int64, ctypes.c_void_p
+    lib.pth_bench_read_groups.restype = f32
+    lib.pth_bench_read_groups.argtypes = [vp, i64, i32, i32, vp, i32, i32, vp, i32, vp]
+    lib.pth_bench_mfma.restype = f32
+    lib.pth_bench_mfma.argtypes = [i32, i32, vp, i32, vp]
+    return lib
+
+
+def read_ceiling(cache, seq_lens, cus: int, reps: int = 10) -> dict:
+    """The headline's exact cache bytes (every cached token's slot row of 8
+    cells), read with the attention kernel's load pattern and discarded."""
     import torch
-    src = torch.empty(mib << 20, dtype=torch.uint8, device="cuda:0")
-    dst = torch.empty_like(src)
-    dst.copy_(src)
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(reps):
-        dst.copy_(src)
-    e1.record()
-    torch.cuda.synchronize()
-    sec = e0.elapsed_time(e1) / reps * 1e-3
-    gbs = 2 * src.numel() / sec / 1e9
-    del src, dst
-    return {"value": round(gbs, 1), "unit": "GB/s",
-            "what": f"device copy of {mib} MiB, read + write bytes / time",
-            "frac_of_peak": round(gbs / PEAK_HBM_GBS, 4)}
+
+    groups = []
+    bt = cache.block_table.cpu()
+    for r, L in enumerate(seq_lens):
+        for blk in range((L + 15) // 16):
+            groups.append((int(bt[r, blk]), min(16, L - 16 * blk)))
+    g = torch.tensor(groups, dtype=torch.int32, device="cuda:0")
+    sink = torch.zeros(1, dtype=torch.int32, device="cuda:0")
+    row = cache.Hkv * (2 * cache.D + 8)
+    stream = torch.cuda.current_stream()
+    ms = bench_lib().pth_bench_read_groups(cache.k_cache.data_ptr(), cache.k_cache.stride(0), 0, row,
+                                           g.data_ptr(), len(groups), cus, sink.data_ptr(), reps,
+                                           stream.cuda_stream)
+    if ms <= 0:
+        raise RuntimeError(f"read ceiling failed ({ms})")
+    byts = sum(n for _, n in groups) * row
+    gbs = byts / (ms * 1e-3) / 1e9
+    return {"value": round(gbs, 1), "unit": "GB/s", "frac_of_peak": round(gbs / PEAK_HBM_GBS, 4),
+            "bytes": byts, "us": round(ms * 1e3, 2),
+            "what": "bench_hip/ceilings.hip read_groups: config 2's cache bytes, whole slot rows "
+                    "in 16-byte register loads, two 16-key groups in flight per work-group, "
+                    f"one work-group per CU, mean of {reps} launches"}
+
+
+def mfma_ceiling(cus: int, iters: int = 20000, reps: int = 5) -> dict:
+    """Dense bf16 MFMA rate (v_mfma_f32_16x16x32_bf16) at 8 waves per CU."""
+    import torch
+
+    sink = torch.zeros(1, device="cuda:0")
+    ms = bench_lib().pth_bench_mfma(cus, iters, sink.data_ptr(), reps,
+                                    torch.cuda.current_stream().cuda_stream)
+    if ms <= 0:
+        raise RuntimeError(f"mfma ceiling failed ({ms})")
+    flops = cus * 8 * iters * 8 * 16 * 16 * 32 * 2
+    tf = flops / (ms * 1e-3) / 1e12
+    return {"value": round(tf, 1), "unit": "TFLOP/s", "frac_of_peak": round(tf / PEAK_BF16_TFLOPS, 4),
+            "what": "bench_hip/ceilings.hip mfma_loop: v_mfma_f32_16x16x32_bf16, 8 waves per CU, "
+                    "8 independent accumulators per wave"}
 
 
 # The reference's published kernel rows closest to this path (its
@@ -269,15 +345,192 @@ def reference_row(name: str, steps: int, warmup: int) -> dict:
                        "plan": {"wm": plan.wm, "num_splits": S}}}
 
 
+ROTATE_BYTES = 1 << 30  # inputs smaller than this are rotated over copies
+
+
+def _copy_inputs(cache, q, qsl):
+    """A second set of the same inputs in fresh device memory."""
+    import dataclasses
+
+    from pth_flash_attn.cache import carve_views
+
+    storage = cache.storage.clone()
+    k, v, ks, vs = carve_views(storage, num_blocks=cache.num_blocks, block_size=cache.block_size,
+                               Hkv=cache.Hkv, D=cache.D, layout=cache.layout,
+                               pad_page_bytes=cache.pad_page_bytes,
+                               offset_bytes=cache.offset_bytes)
+    c = dataclasses.replace(cache, storage=storage, k_cache=k, v_cache=v, k_scale=ks,
+                            v_scale=vs, block_table=cache.block_table.clone(),
+                            seq_lens=cache.seq_lens.clone())
+    return c, q.clone(), qsl.clone()
+
+
+def _events_ms(stream, n, fn) -> float:
+    """Mean ms of n calls of fn() on `stream` (HIP events, synchronised)."""
+    import torch
+
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for i in range(n):
+        fn(i)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / n
+
+
+def measure_config(config: int, query_tokens: int, steps: int, warmup: int, cpu_threads: int,
+                   cus: int, graph: bool = True, keep_inputs: bool = False) -> dict:
+    """One BASELINE configuration through the op: see the module docstring."""
+    import statistics
+
+    import torch
+
+    from pth_flash_attn import capi, ops, planner
+    from pth_flash_attn.cache import build_cache, make_queries
+
+    dev = "cuda:0"
+    name, q_lens, seq_lens, Hq, Hkv, window, is_prefill = workload(config, query_tokens)
+    G, D, BS = Hq // Hkv, 128, 16
+    cache = build_cache(seq_lens, Hkv=Hkv, D=D, block_size=BS, seed=config, device=dev)
+    q, qsl = make_queries(q_lens, Hq=Hq, D=D, seed=config + 100, device=dev)
+    T, R, q_max = len(q), len(q_lens), max(q_lens)
+    ws_ts = planner.workspace_token_splits(max_num_seqs=R, q_dec_max=q_max if not is_prefill else 1,
+                                           Hkv=Hkv, D=D, num_sms=cus)
+    plan = planner.plan_launch(num_tokens=T, num_reqs=R, max_query_len=q_max, G=G, Hkv=Hkv, D=D,
+                               num_sms=cus, is_prefill=is_prefill, ws_token_splits=max(ws_ts, T),
+                               window=window)
+    S = plan.num_splits
+    out = torch.empty_like(q)
+    ws_o = torch.empty(plan.ws_o_shape if S > 1 else (0,), device=dev)
+    ws_lse = torch.empty(plan.ws_lse_shape if S > 1 else (0,), device=dev)
+    scale = 1.0 / math.sqrt(D)
+    in_bytes = cache.storage.numel() + q.numel() * q.element_size()
+    copies = 1 if in_bytes >= ROTATE_BYTES else -(-ROTATE_BYTES // in_bytes) + 1
+    sets = [(cache, q, qsl)] + [_copy_inputs(cache, q, qsl) for _ in range(copies - 1)]
+
+    def step(i):
+        c, qq, ql = sets[i % copies]
+        ops.pth_flash_attn_fwd(out, qq, c.k_cache, c.v_cache, c.k_scale, c.v_scale,
+                               c.block_table, c.seq_lens, ql, q_max, plan.wm, S, scale,
+                               ws_o, ws_lse, window, True)
+
+    stream = torch.cuda.current_stream()
+    # Untimed warm-up: W steps, continued until they add up to WARMUP_MIN_S of
+    # GPU work (the clocks and the TLBs settle; about 4 % slower on config 2
+    # after 4 ms).
+    warm_t0 = time.perf_counter()
+    warm = 0
+    while warm < warmup or time.perf_counter() - warm_t0 < WARMUP_MIN_S:
+        step(warm)
+        warm += 1
+        if warm % 10 == 0:
+            torch.cuda.synchronize()
+    # Exactly `steps` layer calls, synchronised on both sides.
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ms = _events_ms(stream, steps, step)
+    wall = time.perf_counter() - t0
+
+    # The same layer calls replayed from a captured graph (the reference times
+    # graph-replayed launches): the median over replays of 20 calls each.
+    graph_us = None
+    if graph:
+        per_graph = 20
+        g = torch.cuda.CUDAGraph()
+        cap = torch.cuda.Stream()
+        cap.wait_stream(stream)
+        with torch.cuda.stream(cap):
+            step(0)
+            cap.synchronize()
+            with torch.cuda.graph(g, stream=cap):
+                for i in range(per_graph):
+                    step(i)
+        stream.wait_stream(cap)
+        for _ in range(3):
+            g.replay()
+        torch.cuda.synchronize()
+        reps = []
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        for _ in range(max(5, min(30, 2 * steps // per_graph))):
+            e0.record(stream)
+            g.replay()
+            e1.record(stream)
+            e1.synchronize()
+            reps.append(e0.elapsed_time(e1) / per_graph)
+        graph_us = statistics.median(reps) * 1e3
+        del g
+
+    # The two kernels of a layer call alone, through the C ABI exactly as the
+    # op launches them, on the same stream.
+    lib = capi.AttnLib()
+    bq = 16 * plan.wm // G
+    if 1 <= q_max < bq and planner.wm_for_rows(q_max * G) == plan.wm:
+        bq = q_max
+    arg_sets = [capi.attn_args(q=qq, out=out, k_cache=c.k_cache, v_cache=c.v_cache,
+                               k_scale=c.k_scale, v_scale=c.v_scale, block_table=c.block_table,
+                               seq_lens=c.seq_lens, query_start_loc=ql, bq=bq, num_splits=S,
+                               softmax_scale=scale, ws_o=ws_o, ws_lse=ws_lse, window=window)
+                for c, qq, ql in sets]
+    sp = stream.cuda_stream
+    attn_ms = _events_ms(stream, steps, lambda i: lib.check(lib.attention_kernel(arg_sets[i % copies], sp)))
+    comb_ms = None
+    if S > 1:
+        comb_ms = _events_ms(stream, steps, lambda i: lib.check(lib.combine_kernel(arg_sets[0], sp)))
+
+    byts, attn_bytes, flops = algorithmic(q_lens, seq_lens, Hq, Hkv, window)
+    res = {
+        "workload": name, "config": config, "query_tokens_per_request": q_max if config == 3 else None,
+        "num_seqs": R, "query_tokens": T, "context_tokens": sum(seq_lens), "window": window,
+        "plan": {"wm": plan.wm, "num_splits": S},
+        "us_per_layer_call": round(ms * 1e3, 2),
+        "us_per_layer_call_graph_median": None if graph_us is None else round(graph_us, 2),
+        "kernels_us": {"attention": round(attn_ms * 1e3, 2),
+                       "combine": None if comb_ms is None else round(comb_ms * 1e3, 2)},
+        "algorithmic_bytes": byts, "flops": flops,
+        "gbs": round(byts / (ms * 1e-3) / 1e9, 1),
+        "cold": {"input_copies": copies, "input_bytes": in_bytes,
+                 "note": ("inputs rotated over copies: >= 1 GiB between reuses" if copies > 1
+                          else "inputs exceed 1 GiB: read once per call")},
+        "steps": steps, "warmup_steps_run": warm, "wall_s": round(wall, 3),
+    }
+    if is_prefill:
+        tf = flops / (attn_ms * 1e-3) / 1e12
+        res["roofline"] = {"bound": "mfma", "achieved": round(tf, 1), "peak": PEAK_BF16_TFLOPS,
+                           "unit": "TFLOP/s", "frac": round(tf / PEAK_BF16_TFLOPS, 4)}
+        res["tflops"] = round(flops / (ms * 1e-3) / 1e12, 1)
+    else:
+        gbs = attn_bytes / (attn_ms * 1e-3) / 1e9
+        res["roofline"] = {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
+                           "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
+                           "algorithmic_bytes": attn_bytes,
+                           "traffic": profile_traffic("attn_fwd_d128", name)}
+    res["pct_of_peak_hbm"] = round(100.0 * res["gbs"] / PEAK_HBM_GBS, 2)
+    if cpu_threads > 0:
+        res["cpu_baseline"] = cpu_baseline(cache, q, qsl, q_lens, seq_lens, Hq, Hkv, window,
+                                           cpu_threads)
+    if keep_inputs:
+        res["_inputs"] = (cache, seq_lens)
+    del sets, arg_sets, out, ws_o, ws_lse
+    return res
+
+
+# The five BASELINE configurations, config 3 at both query counts.
+ALL_CONFIGS = ((1, 1), (2, 1), (3, 1), (3, 4), (4, 1), (5, 1))
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--config", type=int, default=2)
+    ap.add_argument("--config", type=int, default=2,
+                    help="the headline configuration (default 2, BASELINE's metric)")
     ap.add_argument("--query-tokens", type=int, default=1,
                     help="config 3 only: 1 (decode) or 4 (MTP verify)")
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
+    ap.add_argument("--only-headline", action="store_true",
+                    help="measure the headline configuration only (no configs array, no ceilings)")
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--reference-row", choices=sorted(REFERENCE_ROWS),
                     help="time one of the reference's published rows instead of a config")
@@ -302,122 +555,71 @@ def main() -> int:
         print(json.dumps({"copy_probe_bytes": src.numel(), "launches": a.steps}))
         return 0
 
-    from pth_flash_attn import capi, ops, planner
-    from pth_flash_attn.cache import build_cache, make_queries
+    from pth_flash_attn import ops
 
-    if a.reference_row:
-        if not ops.is_available():
-            raise SystemExit("pth_flash_attn op library is not built")
-        torch.cuda.set_device(0)
-        print(json.dumps(reference_row(a.reference_row, a.steps * 4, a.warmup)))
-        return 0
     if not ops.is_available():
         raise SystemExit("pth_flash_attn op library is not built (python pth-flash-attn_amd/build.py)")
-    dev = "cuda:0"
     torch.cuda.set_device(0)
-    name, q_lens, seq_lens, Hq, Hkv, window, is_prefill = workload(a.config, a.query_tokens)
-    G, D, BS = Hq // Hkv, 128, 16
-    cache = build_cache(seq_lens, Hkv=Hkv, D=D, block_size=BS, seed=a.config, device=dev)
-    q, qsl = make_queries(q_lens, Hq=Hq, D=D, seed=a.config + 100, device=dev)
-    T, R, q_max = len(q), len(q_lens), max(q_lens)
+    if a.reference_row:
+        print(json.dumps(reference_row(a.reference_row, a.steps * 4, a.warmup)))
+        return 0
     cus = torch.cuda.get_device_properties(0).multi_processor_count
-    ws_ts = planner.workspace_token_splits(max_num_seqs=R, q_dec_max=q_max if not is_prefill else 1,
-                                           Hkv=Hkv, D=D, num_sms=cus)
-    plan = planner.plan_launch(num_tokens=T, num_reqs=R, max_query_len=q_max, G=G, Hkv=Hkv, D=D,
-                               num_sms=cus, is_prefill=is_prefill, ws_token_splits=max(ws_ts, T),
-                               window=window)
-    S = plan.num_splits
-    out = torch.empty_like(q)
-    ws_o = torch.empty(plan.ws_o_shape if S > 1 else (0,), device=dev)
-    ws_lse = torch.empty(plan.ws_lse_shape if S > 1 else (0,), device=dev)
-    scale = 1.0 / math.sqrt(D)
-
-    def step():
-        ops.pth_flash_attn_fwd(out, q, cache.k_cache, cache.v_cache, cache.k_scale, cache.v_scale,
-                               cache.block_table, cache.seq_lens, qsl, q_max, plan.wm, S, scale,
-                               ws_o, ws_lse, window, True)
-
-    stream = torch.cuda.current_stream()
-    # Untimed warm-up: the W steps asked for, continued until they add up to
-    # WARMUP_MIN_S of GPU work, so that the first timed steps do not run while
-    # the clocks and the TLBs settle (about 4 % slower on config 2 after 4 ms).
-    warm_t0 = time.perf_counter()
-    warm_steps = 0
-    while warm_steps < a.warmup or time.perf_counter() - warm_t0 < WARMUP_MIN_S:
-        step()
-        warm_steps += 1
-        if warm_steps % 10 == 0:
-            torch.cuda.synchronize()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
-    for _ in range(a.steps):
-        step()
-    e1.record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    ms = e0.elapsed_time(e1) / a.steps
-
-    # The attention kernel alone (the dominant kernel), launched through the C
-    # ABI exactly as the op launches it, on the same stream.
-    lib = capi.AttnLib()
-    bq = 16 * plan.wm // G
-    if 1 <= q_max < bq and planner.wm_for_rows(q_max * G) == plan.wm:
-        bq = q_max
-    args = capi.attn_args(q=q, out=out, k_cache=cache.k_cache, v_cache=cache.v_cache,
-                          k_scale=cache.k_scale, v_scale=cache.v_scale,
-                          block_table=cache.block_table, seq_lens=cache.seq_lens,
-                          query_start_loc=qsl, bq=bq, num_splits=S, softmax_scale=scale,
-                          ws_o=ws_o, ws_lse=ws_lse, window=window)
-    sp = stream.cuda_stream
-    e0.record(stream)
-    for _ in range(a.steps):
-        lib.check(lib.attention_kernel(args, sp))
-    e1.record(stream)
-    torch.cuda.synchronize()
-    attn_ms = e0.elapsed_time(e1) / a.steps
-    # The split combine as the op launches it (it reads only the splits each
-    # request used): the layer-call minus the attention kernel.
-    comb_ms = max(ms - attn_ms, 0.0) if S > 1 else None
-
-    byts, attn_bytes, flops = algorithmic(q_lens, seq_lens, Hq, Hkv, window)
-    gbs = byts / (ms * 1e-3) / 1e9
-    attn_gbs = attn_bytes / (attn_ms * 1e-3) / 1e9
-    traffic = profile_traffic("attn_fwd_d128", name)
+    threads = 0 if a.no_cpu else (a.cpu_threads or min(16, os.cpu_count() or 1))
+    t_start = time.perf_counter()
+    head = measure_config(a.config, a.query_tokens, a.steps, a.warmup, threads, cus,
+                          keep_inputs=True)
+    cache, seq_lens = head.pop("_inputs")
     result = {
         "metric": METRIC,
-        "value": round(gbs, 1),
+        "value": head["gbs"],
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": a.steps,
         "warmup": a.warmup,
-        "warmup_steps_run": warm_steps,
-        "ms_per_step": round(ms, 5),
-        "us_per_layer_call": round(ms * 1e3, 2),
-        "pct_of_peak_hbm": round(100.0 * gbs / PEAK_HBM_GBS, 2),
+        "warmup_steps_run": head["warmup_steps_run"],
+        "ms_per_step": round(head["us_per_layer_call"] / 1e3, 5),
+        "us_per_layer_call": head["us_per_layer_call"],
+        "us_per_layer_call_graph_median": head["us_per_layer_call_graph_median"],
+        "pct_of_peak_hbm": head["pct_of_peak_hbm"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int8 KV / bf16 q,out / fp32 accumulate",
         "data": "synthetic (seeded N(0,1) K/V quantised by the vLLM int8 writer rule, bf16 q)",
-        "config": {"workload": name, "num_seqs": R, "query_tokens": T, "Hq": Hq, "Hkv": Hkv,
-                   "D": D, "block_size": BS, "context_tokens": sum(seq_lens), "window": window,
-                   "plan": {"wm": plan.wm, "num_splits": S}, "parallelism": "single GPU"},
-        "kernels_us": {"attention": round(attn_ms * 1e3, 2),
-                       "combine_and_launch_gaps": None if comb_ms is None else round(comb_ms * 1e3, 2)},
-        "roofline": {"bound": "hbm", "achieved": round(attn_gbs, 1), "peak": PEAK_HBM_GBS,
-                     "unit": "GB/s", "frac": round(attn_gbs / PEAK_HBM_GBS, 4),
-                     "traffic": traffic, "algorithmic_bytes": attn_bytes},
-        "wall_s": round(wall, 3),
+        "config": {"workload": head["workload"], "num_seqs": head["num_seqs"],
+                   "query_tokens": head["query_tokens"], "Hq": 32 if a.config != 1 else 4,
+                   "Hkv": 8 if a.config != 1 else 1, "D": 128, "block_size": 16,
+                   "context_tokens": head["context_tokens"], "window": head["window"],
+                   "plan": head["plan"], "parallelism": "single GPU"},
+        "kernels_us": head["kernels_us"],
+        "roofline": head["roofline"],
     }
-    result["roofline"]["copy_ceiling"] = copy_ceiling()
-    if a.config == 5:
-        result["mfma"] = {"flops": flops, "tflops_achieved": round(flops / (ms * 1e-3) / 1e12, 1),
-                          "peak_tflops": PEAK_BF16_TFLOPS}
-    if not a.no_cpu:
-        threads = a.cpu_threads or min(16, os.cpu_count() or 1)
-        result["cpu_baseline"] = cpu_baseline(cache, q, qsl, q_lens, seq_lens, Hq, Hkv, window, threads)
+    if "cpu_baseline" in head:
+        result["cpu_baseline"] = head["cpu_baseline"]
+    if not a.only_headline:
+        if result["roofline"]["bound"] == "hbm":
+            rc = read_ceiling(cache, seq_lens, cus)
+            result["read_ceiling"] = rc
+            result["roofline"]["frac_of_read_ceiling"] = round(
+                result["roofline"]["achieved"] / rc["value"], 4)
+        del cache
+        torch.cuda.empty_cache()
+        mc = mfma_ceiling(cus)
+        result["mfma_ceiling"] = mc
+        configs = []
+        for cfg, qt in ALL_CONFIGS:
+            if (cfg, qt) == (a.config, a.query_tokens):
+                entry = head
+            else:
+                steps = a.steps if cfg != 5 else max(5, a.steps // 5)
+                entry = measure_config(cfg, qt, steps, a.warmup, threads, cus)
+                torch.cuda.empty_cache()
+            if entry["roofline"]["bound"] == "mfma":
+                entry["roofline"]["frac_of_mfma_ceiling"] = round(
+                    entry["roofline"]["achieved"] / mc["value"], 4)
+            configs.append(entry)
+        result["configs"] = configs
+    result["wall_s"] = round(time.perf_counter() - t_start, 1)
     print(json.dumps(result), flush=True)
     return 0
 

@@ -236,6 +236,13 @@ int32_t pth_attn_attention_lse(const PthAttnArgs* args, float* lse,
  * the op's layer call. No counterpart in the reference's ABI. */
 int32_t pth_attn_attention_kernel(const PthAttnArgs* args, void* stream);
 
+/* Benchmark entry: the split combine exactly as the torch op launches it
+ * after pth_attn_attention_kernel of the same `args` (num_splits > 1): it
+ * reads only the splits each row has and skips rows the attention kernel
+ * wrote to args->out itself. Timing it alone separates the two kernels of a
+ * layer call. No counterpart in the reference's ABI. */
+int32_t pth_attn_combine_kernel(const PthAttnArgs* args, void* stream);
+
 /* pth_attn_attention_lse with no allocation and no workspace argument: the
  * split partials live in a static device array of the library (64 MiB per
  * GPU, held from the first call on a device until the process ends) instead

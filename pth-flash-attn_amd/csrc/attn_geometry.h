@@ -48,6 +48,21 @@ constexpr int32_t kGroupUnits = 8;
 // partition counts that many partition work-groups per work-group, so a row
 // tile with fewer units than waves (few KV heads, a single row group) still
 // keeps every wave of the work-group streaming.
+// Whether every byte the cell-view kernels address from one page stays
+// within 32-bit offsets of the page's base: a 16-key group (15 slot strides),
+// any KV head, any stream offset, plus the row the kernel reads there (one
+// head_size-byte K or V row; the scale streams need 4 of those bytes).
+// The cell-view kernels form uint32 offsets, so a layout that reaches 4 GiB
+// must take the 64-bit-address kernels.
+PA_HD bool cell_reach_fits(uint64_t slot_stride, uint64_t head_stride, int32_t num_kv_heads,
+                           uint64_t max_stream_off, int32_t head_size) {
+  const uint64_t lim = uint64_t{1} << 32;
+  const uint64_t reach = 15u * slot_stride +
+                         static_cast<uint64_t>(num_kv_heads - 1) * head_stride +
+                         max_stream_off + static_cast<uint64_t>(head_size);
+  return reach < lim;
+}
+
 PA_HD int32_t group_units(int32_t n_hu) {
   int32_t g = 1;
   while (g < n_hu && g < kGroupUnits) g <<= 1;

@@ -44,8 +44,9 @@ CacheStream cache_stream(const PthAttnStream& s) {
 }
 
 // Fills the cell view of the four streams when they share their strides and
-// every per-lane offset the paged kernel forms (key < 16 of a 16-key group,
-// any KV head, any stream, plus a 128-byte row) fits in 32 bits.
+// every per-lane offset the paged kernels form fits in 32 bits
+// (cell_reach_fits: key < 16 of a 16-key group, any KV head, any stream,
+// plus a head_size-byte row).
 void set_cell_geometry(const PthAttnArgs& a, AttnParams& p) {
   p.cell = false;
   const PthAttnStream* st[4] = {&a.k_cache, &a.v_cache, &a.k_scale, &a.v_scale};
@@ -65,11 +66,11 @@ void set_cell_geometry(const PthAttnArgs& a, AttnParams& p) {
     p.cell_off[i] = static_cast<uint32_t>(off);
     max_off = std::max(max_off, off);
   }
-  const uint64_t reach = 15u * static_cast<uint64_t>(ss) +
-                         static_cast<uint64_t>(a.num_kv_heads - 1) * static_cast<uint64_t>(sh) +
-                         max_off + 128u;
   const uint64_t slot_reach = static_cast<uint64_t>(a.block_size) * static_cast<uint64_t>(ss);
-  if (static_cast<uint64_t>(sb) >= lim || reach >= lim || slot_reach >= lim) return;
+  if (static_cast<uint64_t>(sb) >= lim || slot_reach >= lim ||
+      !cell_reach_fits(static_cast<uint64_t>(ss), static_cast<uint64_t>(sh), a.num_kv_heads,
+                       max_off, a.head_size))
+    return;
   p.cell = true;
   p.cell_base = reinterpret_cast<const char*>(lo);
   p.cell_block = static_cast<uint32_t>(sb);
@@ -517,6 +518,16 @@ int32_t pth_attn_attention_kernel(const PthAttnArgs* args, void* stream) {
   if (rc != PTH_ATTN_OK) return rc;
   return pa::launch_attention(*args, 0, static_cast<hipStream_t>(stream), nullptr, 0, 0,
                               /*fill_unused_splits=*/false);
+}
+
+int32_t pth_attn_combine_kernel(const PthAttnArgs* args, void* stream) {
+  pa::clear_error();
+  const int32_t rc = check_args_abi(args);
+  if (rc != PTH_ATTN_OK) return rc;
+  PA_REQUIRE(args->num_splits > 1, "num_splits must be > 1 (a single split has no combine)");
+  PA_REQUIRE(args->out != nullptr, "out must be non-NULL");
+  return pa::launch_combine(combine_of(*args), static_cast<hipStream_t>(stream), nullptr, 0, 0,
+                            args);
 }
 
 int32_t pth_attn_combine(const PthAttnCombineArgs* args, void* stream) {

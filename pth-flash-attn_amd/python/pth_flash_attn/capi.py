@@ -36,6 +36,7 @@ EXPORTED_SYMBOLS = (
     "pth_attn_attention_lse",
     "pth_attn_attention_kernel",
     "pth_attn_attention_lse_noalloc",
+    "pth_attn_combine_kernel",
     "pth_attn_write_args_bytes",
     "pth_attn_write_kv",
 )
@@ -190,6 +191,8 @@ class AttnLib:
         lib.pth_attn_attention_lse.restype = i32
         lib.pth_attn_attention_lse.argtypes = [
             ctypes.POINTER(PthAttnArgs), vp, ctypes.c_int64, ctypes.c_int64, vp]
+        lib.pth_attn_combine_kernel.restype = i32
+        lib.pth_attn_combine_kernel.argtypes = [ctypes.POINTER(PthAttnArgs), vp]
         lib.pth_attn_attention_lse_noalloc.restype = i32
         lib.pth_attn_attention_lse_noalloc.argtypes = [
             ctypes.POINTER(PthAttnArgs), vp, ctypes.c_int64, ctypes.c_int64, vp]
@@ -214,6 +217,10 @@ class AttnLib:
     def attention_kernel(self, args: PthAttnArgs, stream: int | None = None) -> int:
         """The attention kernel alone, as the torch op launches it (see the header)."""
         return self.lib.pth_attn_attention_kernel(ctypes.byref(args), stream)
+
+    def combine_kernel(self, args: PthAttnArgs, stream: int | None = None) -> int:
+        """The split combine alone, as the torch op launches it (see the header)."""
+        return self.lib.pth_attn_combine_kernel(ctypes.byref(args), stream)
 
     def attention_lse(self, args: PthAttnArgs, lse: Any, stream: int | None = None) -> int:
         """Run attention (+ combine) and write the natural-log LSE into `lse` [T, Hq] fp32."""

@@ -189,11 +189,40 @@ static void streams() {
   std::printf("streams ok\n");
 }
 
+// cell_reach_fits: a layout whose furthest byte is within one row of 4 GiB
+// must be refused for D = 256 rows even when it fits for shorter rows (the
+// 32-bit offsets of the cell kernels would wrap), and the vLLM cell must fit.
+static void cell_reach() {
+  const uint64_t lim = uint64_t{1} << 32;
+  // vLLM NHD cell, 8 heads, D = 128: tiny reach.
+  CHECK(cell_reach_fits(2112, 264, 8, 260, 128), "vLLM cell");
+  // Brute force over head sizes and the last bytes below 4 GiB.
+  const int32_t ds[3] = {64, 128, 256};
+  for (int32_t d : ds) {
+    for (uint64_t gap = 0; gap < 600; ++gap) {
+      // 15 slot strides + 7 head strides + max offset = lim - gap.
+      const uint64_t ss = 200000000, sh = 1000;
+      const uint64_t base = 15 * ss + 7 * sh;
+      const uint64_t max_off = lim - gap - base;
+      const bool want = gap > static_cast<uint64_t>(d);  // last byte read: max_off + d - 1 < lim
+      CHECK(cell_reach_fits(ss, sh, 8, max_off, d) == want, "d=%d gap=%llu", d,
+            static_cast<unsigned long long>(gap));
+    }
+  }
+  // A reach that fits a 128-byte row but not a 256-byte one.
+  const uint64_t ss = 1u << 20, sh = 264;
+  const uint64_t max_off = lim - 15 * ss - 7 * sh - 200;
+  CHECK(cell_reach_fits(ss, sh, 8, max_off, 128), "128-byte rows fit");
+  CHECK(!cell_reach_fits(ss, sh, 8, max_off, 256), "256-byte rows must not fit");
+  std::printf("cell_reach ok\n");
+}
+
 int main() {
   div32();
   row_tiles();
   visible();
   streams();
+  cell_reach();
   std::printf("ALL OK\n");
   return fails;
 }

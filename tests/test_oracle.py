@@ -211,7 +211,7 @@ def test_combine_split_identity():
 
 
 # ---------------------------------------------- the reference's own CPU path
-needs_ref = pytest.mark.skipif(oracle.ref_lib() is None,
+needs_ref = pytest.mark.skipif(not oracle.REF_LIB_PATH.is_file(),
                                reason="oracle/_ref not built (needs /root/reference)")
 
 REF_CASES = [
