@@ -22,9 +22,10 @@ ROCm platform reports it as capability 9.5).
 
 Importing this module imports vLLM; on a host without vLLM it raises
 ImportError (``plugin.register`` imports it only when the backend is
-selected). vLLM is not installed where this library is built and tested, so
-this adapter is untested; ``tests/test_slices.py`` covers the logic it
-delegates to.
+selected). vLLM is not installed where this library is built and tested:
+``tests/test_vllm_backend.py`` executes every class here against stand-ins
+for the vLLM names imported below (``tests/vllm_stub.py``) with a recording
+op, and ``tests/test_slices.py`` covers the logic it delegates to.
 """
 
 from __future__ import annotations
