@@ -348,21 +348,30 @@ def reference_row(name: str, steps: int, warmup: int) -> dict:
 ROTATE_BYTES = 1 << 30  # inputs smaller than this are rotated over copies
 
 
-def _copy_inputs(cache, q, qsl):
-    """A second set of the same inputs in fresh device memory."""
+def _input_copies(cache, q, qsl, n: int) -> list:
+    """n more sets of the same inputs, carved from one allocation per tensor
+    (one copy kernel each, however many sets)."""
     import dataclasses
 
     from pth_flash_attn.cache import carve_views
 
-    storage = cache.storage.clone()
-    k, v, ks, vs = carve_views(storage, num_blocks=cache.num_blocks, block_size=cache.block_size,
-                               Hkv=cache.Hkv, D=cache.D, layout=cache.layout,
-                               pad_page_bytes=cache.pad_page_bytes,
-                               offset_bytes=cache.offset_bytes)
-    c = dataclasses.replace(cache, storage=storage, k_cache=k, v_cache=v, k_scale=ks,
-                            v_scale=vs, block_table=cache.block_table.clone(),
-                            seq_lens=cache.seq_lens.clone())
-    return c, q.clone(), qsl.clone()
+    if n <= 0:
+        return []
+    store = cache.storage.unsqueeze(0).repeat(n, 1)
+    bts = cache.block_table.unsqueeze(0).repeat(n, 1, 1)
+    sls = cache.seq_lens.unsqueeze(0).repeat(n, 1)
+    qs = q.unsqueeze(0).repeat(n, 1, 1, 1)
+    qsls = qsl.unsqueeze(0).repeat(n, 1)
+    sets = []
+    for i in range(n):
+        k, v, ks, vs = carve_views(store[i], num_blocks=cache.num_blocks,
+                                   block_size=cache.block_size, Hkv=cache.Hkv, D=cache.D,
+                                   layout=cache.layout, pad_page_bytes=cache.pad_page_bytes,
+                                   offset_bytes=cache.offset_bytes)
+        c = dataclasses.replace(cache, storage=store[i], k_cache=k, v_cache=v, k_scale=ks,
+                                v_scale=vs, block_table=bts[i], seq_lens=sls[i])
+        sets.append((c, qs[i], qsls[i]))
+    return sets
 
 
 def _events_ms(stream, n, fn) -> float:
@@ -407,7 +416,7 @@ def measure_config(config: int, query_tokens: int, steps: int, warmup: int, cpu_
     scale = 1.0 / math.sqrt(D)
     in_bytes = cache.storage.numel() + q.numel() * q.element_size()
     copies = 1 if in_bytes >= ROTATE_BYTES else -(-ROTATE_BYTES // in_bytes) + 1
-    sets = [(cache, q, qsl)] + [_copy_inputs(cache, q, qsl) for _ in range(copies - 1)]
+    sets = [(cache, q, qsl)] + _input_copies(cache, q, qsl, copies - 1)
 
     def step(i):
         c, qq, ql = sets[i % copies]

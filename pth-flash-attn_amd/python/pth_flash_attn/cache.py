@@ -71,12 +71,14 @@ def carve_views(
     else:
         s_slot, s_head = C, block_size * C
     size = (num_blocks, block_size, Hkv)
-    k = torch.as_strided(storage, (*size, D), (page, s_slot, s_head, 1), offset_bytes)
-    v = torch.as_strided(storage, (*size, D), (page, s_slot, s_head, 1), offset_bytes + D + 4)
+    # as_strided offsets are absolute within the underlying storage, so a
+    # storage that is itself a view (a slice of a larger buffer) adds its own.
+    base = storage.storage_offset() + offset_bytes
+    k = torch.as_strided(storage, (*size, D), (page, s_slot, s_head, 1), base)
+    v = torch.as_strided(storage, (*size, D), (page, s_slot, s_head, 1), base + D + 4)
     f32 = torch.tensor([], dtype=torch.float32, device=storage.device).set_(
         storage.untyped_storage()
     )
-    base = storage.storage_offset() + offset_bytes
     w = SCALE_BYTES
     ks = torch.as_strided(f32, size, (page // w, s_slot // w, s_head // w), (base + D) // w)
     vs = torch.as_strided(f32, size, (page // w, s_slot // w, s_head // w), (base + 2 * D + 4) // w)

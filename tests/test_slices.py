@@ -437,3 +437,15 @@ def test_without_vllm_register_and_the_backend_raise_import_error():
         plugin.register()
     with pytest.raises(ImportError):
         importlib.import_module("pth_flash_attn.vllm_backend")
+
+
+def test_carve_views_of_a_slice_of_a_larger_buffer():
+    """Views carved from a storage that is itself a slice (bench.py rotates
+    input copies carved from one allocation) address that slice's bytes."""
+    c = build_cache([100, 37], Hkv=2, D=128, block_size=16, seed=1)
+    big = c.storage.unsqueeze(0).repeat(3, 1)
+    big[0].fill_(7)
+    for i in (1, 2):
+        got = carve_views(big[i], num_blocks=c.num_blocks, block_size=16, Hkv=2, D=128)
+        for g, w in zip(got, (c.k_cache, c.v_cache, c.k_scale, c.v_scale)):
+            assert torch.equal(g, w)
