@@ -39,6 +39,45 @@
 namespace pa {
 namespace {
 
+// PV operands of the row-block kernel are fp16: V as int8 -> fp16 (exact)
+// and P'' = fp16(p vs 2^-C), the reference's precision class (reference
+// softmax.cuh:91-170: fp16 P with the V scale folded in and a running
+// V-scale exponent). C is the wave's running exponent of the largest V scale
+// seen (every chunk's V scales < 2^C), so p vs 2^-C < 2^8 (p <= 2^8 under the
+// lazy rescale) and fits fp16; when a chunk raises C, O is rescaled by
+// 2^(C_old - C_new). fp16 keeps 11 significant bits against bf16's 8, so one
+// PV product per operand suffices (the decode kernels, bandwidth-bound, keep
+// their bf16 hi + lo pair).
+__device__ __forceinline__ f32x4 mfma_f16(f16x8 a, f16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+// Byte j of each of eight 8-byte runs -> eight fp16 (exact for int8).
+__device__ __forceinline__ f16x8 column_to_f16(const u32x2 (&v)[8], int j) {
+  const int w = j >> 2, b = j & 3;
+  f16x8 r;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) r[e] = static_cast<_Float16>(i8_to_f32(v[e][w], b));
+  return r;
+}
+// The running V-scale exponent before any chunk: no scale seen yet.
+constexpr int kNoExp = -1000;
+// The exponent e of a largest V scale v (v < 2^e), clamped to [-125, 126]
+// (2^-e a normal float); kNoExp for v = 0 (every key masked). Wave-uniform.
+__device__ __forceinline__ int vscale_exp(float v) {
+  int e = v > 0.0f ? static_cast<int>((__builtin_bit_cast(uint32_t, v) >> 23) & 0xff) - 126
+                   : kNoExp;
+  e = e == kNoExp ? e : (e < -125 ? -125 : (e > 126 ? 126 : e));
+  return __builtin_amdgcn_readfirstlane(e);
+}
+// After a wave's last chunk: O is in units of 2^-C, so O / (l 2^-C) is the
+// output and m + C + log2(l 2^-C) = m + log2(l) the row's log2-sum-exp, the
+// form finish() and the key-part merge expect.
+__device__ __forceinline__ void undo_vexp(State& st, int vexp) {
+  if (vexp == kNoExp) return;
+  st.l *= __builtin_ldexpf(1.0f, -vexp);
+  st.m += static_cast<float>(vexp);
+}
+
 constexpr int kRowWaves = kFwdWaves;              // waves per work-group
 constexpr int kWaveRows = 2 * kRowsPerWave;       // rows per wave
 constexpr int kBlockRows = kRowWaves * kWaveRows;  // rows per block
@@ -276,7 +315,7 @@ __device__ __forceinline__ int rows_chunk_loads(int mask, int rs) {
 template <bool kF16Q, bool kBoth, class Ops>
 __device__ __forceinline__ void compute_rows(const RowSet& R, const Lanes (&L)[2], int c, Ops& ops,
                                              const bf16x8 (&qb)[2][4], const bf16x8 (&qlo)[2][4],
-                                             float scl, State (&st)[2]) {
+                                             float scl, State (&st)[2], int& vexp, float& vlim) {
   float ks[8], vs[8];
   ops.scales(scl, ks, vs);
   const int ng = kBoth || R.two ? 2 : 1;
@@ -309,7 +348,8 @@ __device__ __forceinline__ void compute_rows(const RowSet& R, const Lanes (&L)[2
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) t[i][4 * sub + e] = fmaf(acc[i][e], ks[4 * sub + e], -m_use[i]);
+      for (int e = 0; e < 4; ++e)
+        t[i][4 * sub + e] = fmaf(acc[i][e], ks[4 * sub + e], -m_use[i]);
   }
   __builtin_amdgcn_s_setprio(0);
   ops.load_v();
@@ -326,7 +366,43 @@ __device__ __forceinline__ void compute_rows(const RowSet& R, const Lanes (&L)[2
         if (key < L[i].lo || key > L[i].hi) t[i][e] = kNegInf;
     }
   }
-  bf16x8 p_hi[2], p_lo[2];
+  // The V scales times 2^-C (C: the running exponent; every V scale seen so
+  // far is below 2^C), so that p vs 2^-C < 2^8 fits fp16; O is kept in units
+  // of 2^-C and rescaled when C grows (undo_vexp folds 2^C back in).
+  if constexpr (Ops::kNormalised) {
+    const int e = ops.vexp();  // normalised by the converting wave
+    if (e > vexp) {
+      if (vexp != kNoExp) {
+        const float f = __builtin_ldexpf(1.0f, vexp - e);
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int j = 0; j < 8; ++j) st[i].o[j] *= f;
+      }
+      vexp = e;
+    }
+  } else {
+    // A V scale of this chunk at or above 2^C (masked keys have 0): raise C
+    // to the chunk's largest.
+    if (__ballot(max8_raw(vs) >= vlim) != 0) {
+      const int e = vscale_exp(xor_max(max8_raw(vs)));
+      if (e > vexp) {
+        if (vexp != kNoExp) {
+          const float f = __builtin_ldexpf(1.0f, vexp - e);
+#pragma unroll
+          for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) st[i].o[j] *= f;
+        }
+        vexp = e;
+        vlim = __builtin_ldexpf(1.0f, e);
+      }
+    }
+    const float vnorm = __builtin_ldexpf(1.0f, vexp == kNoExp ? 0 : -vexp);
+#pragma unroll
+    for (int e2 = 0; e2 < 8; ++e2) vs[e2] *= vnorm;
+  }
+  f16x8 p16[2];
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     if (i >= ng) continue;
@@ -352,38 +428,24 @@ __device__ __forceinline__ void compute_rows(const RowSet& R, const Lanes (&L)[2
     }
     st[i].l += lsum;
 #pragma unroll
-    for (int e = 0; e < 8; e += 2) {
-      const bf16x2 h = pack_bf16(pv[e], pv[e + 1]);
-      const uint32_t hb = __builtin_bit_cast(uint32_t, h);
-      const float h0 = __builtin_bit_cast(float, hb << 16);
-      const float h1 = __builtin_bit_cast(float, hb & 0xffff0000u);
-      const bf16x2 lw = pack_bf16(pv[e] - h0, pv[e + 1] - h1);
-      p_hi[i][e] = h[0];
-      p_hi[i][e + 1] = h[1];
-      p_lo[i][e] = lw[0];
-      p_lo[i][e + 1] = lw[1];
-    }
+    for (int e = 0; e < 8; ++e) p16[i][e] = static_cast<_Float16>(pv[e]);
   }
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
-    const bf16x8 vcol = ops.v(j);
+    const f16x8 vcol = ops.v(j);
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      if (i < ng) {
-        st[i].o[j] = mfma(vcol, p_hi[i], st[i].o[j]);
-        st[i].o[j] = mfma(vcol, p_lo[i], st[i].o[j]);
-      }
-    }
+    for (int i = 0; i < 2; ++i)
+      if (i < ng) st[i].o[j] = mfma_f16(vcol, p16[i], st[i].o[j]);
   }
 }
 
 // ---------------------------------------------------------------------------
 // Wide blocks (one key part: all 8 waves compute every chunk). The int8 ->
-// bf16 conversion is shared: each wave converts one eighth of a chunk into a
-// bf16 copy in LDS, one chunk ahead of the compute, and every wave reads its
+// bf16 / fp16 conversion is shared: each wave converts one eighth of a chunk
+// into a copy in LDS, one chunk ahead of the compute, and every wave reads its
 // MFMA operands from the copy. Copy layout (16 KB, lane-contiguous):
 //   K: [sub 2][j 4][lane 64] x 16 B  -- bf16 K[16 sub + (l % 16)][32 (l / 16) + 8 j ..]
-//   V: [j 8][lane 64] x 16 B         -- bf16 V[tv(e)][8 (l % 16) + j], e = 0..7
+//   V: [j 8][lane 64] x 16 B         -- fp16 V[tv(e)][8 (l % 16) + j], e = 0..7
 // Wave w converts K operand (sub, j) = (w / 4, w % 4) and V column j = w.
 // A wide block advances two chunks per barrier step: step s computes chunks
 // 2s, 2s + 1, converts chunks 2s + 2, 2s + 3 and issues the loads of chunks
@@ -391,9 +453,11 @@ __device__ __forceinline__ void compute_rows(const RowSet& R, const Lanes (&L)[2
 // chunks 2s - 2, 2s - 1 left.
 constexpr int kWideSlots = 8;  // int8 chunk slots of a wide block
 constexpr int kCopyBytes = 16384;
-constexpr int kCopies = 4;     // bf16 copies: the pair computed and the pair converted
+constexpr int kCopies = 4;     // copies: the pair computed and the pair converted
 constexpr int kCopyBase = kWideSlots * kSlotBytes;
-static_assert(kCopyBase + kCopies * kCopyBytes <= kRowSlots * kSlotBytes, "wide-block LDS");
+// The exponent C each copy's V scales were normalised by (one int per copy).
+constexpr int kCopyExp = kCopyBase + kCopies * kCopyBytes;
+static_assert(kCopyExp + 4 * kCopies <= kRowSlots * kSlotBytes, "wide-block LDS");
 
 __device__ __forceinline__ uint32_t ds_read_i8(uint32_t a) {
   uint32_t v;
@@ -406,6 +470,19 @@ __device__ __forceinline__ void ds_write4(uint32_t a, float v) {
 template <int kOff>
 __device__ __forceinline__ void ds_write16(uint32_t a, u32x4 v) {
   asm volatile("ds_write_b128 %0, %1 offset:%2" ::"v"(a), "v"(v), "n"(kOff) : "memory");
+}
+
+template <int kCtrl>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v),
+                                                               kCtrl, 0xf, 0xf, false));
+}
+// Max over each row of 16 lanes (DPP; every lane of the row gets it).
+__device__ __forceinline__ float wave_max16(float x) {
+  x = fmaxf(x, dpp_mov<0xB1>(x));   // quad_perm [1, 0, 3, 2]
+  x = fmaxf(x, dpp_mov<0x4E>(x));   // quad_perm [2, 3, 0, 1]
+  x = fmaxf(x, dpp_mov<0x141>(x));  // row_half_mirror
+  return fmaxf(x, dpp_mov<0x140>(x));  // row_mirror
 }
 
 // Per-lane LDS offsets of the conversion reads (chunk slot relative).
@@ -424,16 +501,40 @@ __device__ __forceinline__ ConvOffsets conv_offsets(int wave, int lane) {
   return o;
 }
 
-// Wave `wave`'s eighth of the chunk in int8 slot `slot` -> bf16 copy `copy`.
+// The running V-scale exponent of a wide block's chunks, kept by its
+// converting wave: every V scale of the block's keys converted so far is
+// below lim = 2^exp (lim = 0 before the first).
+struct VScaleBound {
+  int exp = kNoExp;
+  float lim = 0.0f;
+};
+
+// Wave `wave`'s eighth of the chunk in int8 slot `slot` -> copy `copy` (K in
+// bf16, V in fp16). The last wave also prepares the chunk's scales in place:
+// the K scales times scale * log2 e (the product the chunk step would form
+// per lane), the V scales times 2^-C with C = vb.exp after this chunk (keys
+// outside [ld_lo, ld_hi) are masked by every row and do not count), and
+// writes C to `cslot` for the computing waves (vbd: the block's bound).
 __device__ __forceinline__ void convert_share(uint32_t slot, uint32_t copy, const ConvOffsets& o,
-                                              float scale_log2, int wave, int lane) {
-  if (wave == kRowWaves - 1 && lane < kChunkTokens) {
-    // The chunk's K scales, in place: times scale * log2 e (the product the
-    // chunk step would form per lane).
-    const uint32_t sa = slot + kSlotScale + 4 * lane;
+                                              float scale_log2, int wave, int lane, int key0,
+                                              int ld_lo, int ld_hi, VScaleBound& vbd,
+                                              uint32_t cslot) {
+  if (wave == kRowWaves - 1) {
+    const uint32_t sa = slot + kSlotScale + 4 * lane;  // K scales, then V scales
     float x = ds_read4(sa);
     asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(x) : : "memory");
-    ds_write4(sa, x * scale_log2);
+    const int key = key0 + (lane & (kChunkTokens - 1));
+    const float v = lane >= kChunkTokens && key >= ld_lo && key < ld_hi ? x : 0.0f;
+    if (__ballot(v >= vbd.lim) != 0) {  // a scale at or above the bound: raise it
+      const int e = vscale_exp(xor_max(wave_max16(v)));
+      if (e > vbd.exp) {
+        vbd.exp = e;
+        vbd.lim = __builtin_ldexpf(1.0f, e);
+      }
+    }
+    ds_write4(sa, lane < kChunkTokens ? x * scale_log2
+                                      : x * __builtin_ldexpf(1.0f, vbd.exp == kNoExp ? 0 : -vbd.exp));
+    if (lane == 0) asm volatile("ds_write_b32 %0, %1" ::"v"(cslot), "v"(vbd.exp) : "memory");
   }
   u32x2 kw = ds_read8<0>(slot + o.k);
   uint32_t vb[8];
@@ -449,12 +550,10 @@ __device__ __forceinline__ void convert_share(uint32_t slot, uint32_t copy, cons
                : "memory");
   const bf16x8 ka = i8x8_to_bf16(kw[0], kw[1]);
   // V column: the 8 keys in e order (tv(e) = 16 (e / 4) + 4 g + e % 4).
-  bf16x2 pr[4];
+  f16x8 va;
 #pragma unroll
-  for (int e = 0; e < 4; ++e)
-    pr[e] = pack_bf16(static_cast<float>(static_cast<int32_t>(vb[2 * e])),
-                      static_cast<float>(static_cast<int32_t>(vb[2 * e + 1])));
-  const bf16x8 va = {pr[0][0], pr[0][1], pr[1][0], pr[1][1], pr[2][0], pr[2][1], pr[3][0], pr[3][1]};
+  for (int e = 0; e < 8; ++e)
+    va[e] = static_cast<_Float16>(static_cast<float>(static_cast<int32_t>(vb[e])));
   const uint32_t dst = copy + wave * 1024 + lane * 16;
   ds_write16<0>(dst, __builtin_bit_cast(u32x4, ka));
   ds_write16<8192>(dst, __builtin_bit_cast(u32x4, va));
@@ -462,6 +561,7 @@ __device__ __forceinline__ void convert_share(uint32_t slot, uint32_t copy, cons
 
 // Operands of compute_rows from the int8 chunk in registers.
 struct Int8Ops {
+  static constexpr bool kNormalised = false;  // V scales as stored: the wave normalises
   const Chunk& ch;
   __device__ __forceinline__ void scales(float scl, float (&ks)[8], float (&vs)[8]) const {
     lane_scales(ch.sc * scl, ks, vs);
@@ -471,22 +571,28 @@ struct Int8Ops {
     return (j & 1) ? i8x8_to_bf16(w[2], w[3]) : i8x8_to_bf16(w[0], w[1]);
   }
   __device__ __forceinline__ void load_v() const {}
-  __device__ __forceinline__ bf16x8 v(int j) const { return column_to_bf16(ch.v, j); }
+  __device__ __forceinline__ f16x8 v(int j) const { return column_to_f16(ch.v, j); }
 };
 
-// Operands of compute_rows from a bf16 copy: K and the scales read at
+// Operands of compute_rows from a converted copy: K and the scales read at
 // construction, V read by load_v. The chunk's K scales in its int8 slot were
 // multiplied by scale * log2 e when it was converted (convert_share), so a
 // lane reads its 8 K and 8 V scales as they are: keys 4 g .. 4 g + 3 and
 // 16 + 4 g .., four 16-byte reads that the 16 lanes of a row share.
 struct CopyOps {
+  static constexpr bool kNormalised = true;  // V scales times 2^-vexp() (convert_share)
   uint32_t a;  // copy + 16 lane
   u32x4 kk[8];
   u32x4 vv[8];
   u32x4 sk[2], sv[2];
 
-  __device__ __forceinline__ CopyOps(uint32_t copy, uint32_t slot, int lane)
+  int cexp;    // the exponent the chunk's V scales were normalised by
+
+  __device__ __forceinline__ int vexp() const { return cexp; }
+  __device__ __forceinline__ CopyOps(uint32_t copy, uint32_t slot, uint32_t cslot, int lane)
       : a(copy + lane * 16) {
+    uint32_t ce;
+    asm volatile("ds_read_b32 %0, %1" : "=v"(ce) : "v"(cslot));
     const uint32_t sa = slot + kSlotScale + 16 * (lane >> 4);
     sk[0] = ds_read16<0>(sa);
     sk[1] = ds_read16<64>(sa);
@@ -502,9 +608,11 @@ struct CopyOps {
     kk[7] = ds_read16<7168>(a);
     asm volatile("s_waitcnt lgkmcnt(0)"
                  : "+v"(kk[0]), "+v"(kk[1]), "+v"(kk[2]), "+v"(kk[3]), "+v"(kk[4]), "+v"(kk[5]),
-                   "+v"(kk[6]), "+v"(kk[7]), "+v"(sk[0]), "+v"(sk[1]), "+v"(sv[0]), "+v"(sv[1])
+                   "+v"(kk[6]), "+v"(kk[7]), "+v"(sk[0]), "+v"(sk[1]), "+v"(sv[0]), "+v"(sv[1]),
+                   "+v"(ce)
                  :
                  : "memory");
+    cexp = __builtin_amdgcn_readfirstlane(static_cast<int>(ce));
   }
   __device__ __forceinline__ void scales(float, float (&ks)[8], float (&vs)[8]) const {
     // Each element goes through a named scalar: a bit cast of a subscripted
@@ -531,14 +639,14 @@ struct CopyOps {
   }
   // The first use waits for all eight (the softmax in between hides the
   // LDS latency).
-  __device__ __forceinline__ bf16x8 v(int j) {
+  __device__ __forceinline__ f16x8 v(int j) {
     if (j == 0)
       asm volatile("s_waitcnt lgkmcnt(0)"
                    : "+v"(vv[0]), "+v"(vv[1]), "+v"(vv[2]), "+v"(vv[3]), "+v"(vv[4]),
                      "+v"(vv[5]), "+v"(vv[6]), "+v"(vv[7])
                    :
                    : "memory");
-    return __builtin_bit_cast(bf16x8, vv[j]);
+    return __builtin_bit_cast(f16x8, vv[j]);
   }
 };
 
@@ -642,6 +750,10 @@ __device__ __forceinline__ void wide_block(const AttnParams& p, const Block& B, 
                                            int wave, int lane) {
   const int len = B.n_chunks;
   if (len == 0) return;
+  int vexp = kNoExp;  // this wave's
+  float vlim = 0.0f;  // (unused with the converted copies)
+  VScaleBound vb;     // the converting wave's
+  auto cslot = [&](int k) { return lds_base + kCopyExp + 4 * (k % kCopies); };
   const int nload = wave == 0 ? 2 : 1;
   const uint32_t copy0 = lds_base + kCopyBase;
   auto slot_of = [&](int k) { return (k % kWideSlots) * kSlotBytes; };
@@ -661,8 +773,11 @@ __device__ __forceinline__ void wide_block(const AttnParams& p, const Block& B, 
     wait_vmcnt_dyn(nload * younger);
   }
   wg_barrier();
-  convert_share(lds_base + slot_of(0), copy0 + copy_of(0), cvo, p.scale_log2, wave, lane);
-  if (1 < len) convert_share(lds_base + slot_of(1), copy0 + copy_of(1), cvo, p.scale_log2, wave, lane);
+  convert_share(lds_base + slot_of(0), copy0 + copy_of(0), cvo, p.scale_log2, wave, lane,
+                chunk_key(0), B.ld_lo, B.ld_hi, vb, cslot(0));
+  if (1 < len)
+    convert_share(lds_base + slot_of(1), copy0 + copy_of(1), cvo, p.scale_log2, wave, lane,
+                  chunk_key(1), B.ld_lo, B.ld_hi, vb, cslot(1));
   for (int k = 0; k < len; k += 2) {
     if (k + 2 < len) {
       // Issued so far: chunks up to min(k + 5, len - 1); k + 2, k + 3 must land.
@@ -676,19 +791,25 @@ __device__ __forceinline__ void wide_block(const AttnParams& p, const Block& B, 
       issue_wide(p, Ld, pp, 0, lds + slot_of(k + 6), wave, lane);
       if (k + 7 < len) issue_wide(p, Ld, pp, 1, lds + slot_of(k + 7), wave, lane);
     }
-    if (k + 2 < len) convert_share(lds_base + slot_of(k + 2), copy0 + copy_of(k + 2), cvo, p.scale_log2, wave, lane);
-    if (k + 3 < len) convert_share(lds_base + slot_of(k + 3), copy0 + copy_of(k + 3), cvo, p.scale_log2, wave, lane);
+    if (k + 2 < len)
+      convert_share(lds_base + slot_of(k + 2), copy0 + copy_of(k + 2), cvo, p.scale_log2, wave,
+                    lane, chunk_key(k + 2), B.ld_lo, B.ld_hi, vb, cslot(k + 2));
+    if (k + 3 < len)
+      convert_share(lds_base + slot_of(k + 3), copy0 + copy_of(k + 3), cvo, p.scale_log2, wave,
+                    lane, chunk_key(k + 3), B.ld_lo, B.ld_hi, vb, cslot(k + 3));
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int kk = k + h;
       const int c = chunk_key(kk);
       if (kk < len && R.has_rows && c <= R.w_hi_max && c + kChunkTokens > R.w_lo_min) {
-        CopyOps ops(copy0 + copy_of(kk), lds_base + slot_of(kk), lane);
-        compute_rows<kF16Q, true>(R, L, c, ops, qb, qlo, scl, st);
+        CopyOps ops(copy0 + copy_of(kk), lds_base + slot_of(kk), cslot(kk), lane);
+        compute_rows<kF16Q, true>(R, L, c, ops, qb, qlo, scl, st, vexp, vlim);
       }
     }
     if (k + 8 < len) pair_pages(p, B, Ld.bt0, chunk_key(k + 8), pp);
   }
+  undo_vexp(st[0], vexp);
+  undo_vexp(st[1], vexp);
 }
 
 template <bool kWindow, bool kF16Q>
@@ -768,6 +889,8 @@ void attn_fwd_rows(const AttnParams p) {
       if (i + 1 < len) rows_pages(p, B, c0 + kChunkTokens * (i + 1), Ld);
     }
     const int nsteps = solo ? len : steps;
+    int vexp = kNoExp;
+    float vlim = 0.0f;  // 2^vexp (0: no V scale seen yet)
     for (int k = 0; k < nsteps; ++k) {
       if (k < len) {
         const int last = k + ahead - 1 < len - 1 ? k + ahead - 1 : len - 1;
@@ -788,9 +911,11 @@ void attn_fwd_rows(const AttnParams p) {
       }
       if (mine) {
         Int8Ops ops{ch};
-        compute_rows<kF16Q, false>(R, L, c, ops, qb, qlo, scl, st);
+        compute_rows<kF16Q, false>(R, L, c, ops, qb, qlo, scl, st, vexp, vlim);
       }
     }
+    undo_vexp(st[0], vexp);
+    undo_vexp(st[1], vexp);
     const int ng = R.two ? 2 : 1;
     if (kp > 1) {
       __syncthreads();  // every wave is done with the slots

@@ -86,9 +86,22 @@ def run_op(b: Batch, *, num_splits: int | None = None):
 
 
 # fp32 outputs carry no storage rounding: the kernel's own arithmetic (exact
-# int8 K/V and q in bf16, fp32 scores, P as a 16-bit hi + lo pair, fp32
-# accumulation) must stay within this of the fp64 oracle.
+# int8 K/V and q in bf16, fp32 scores, fp32 accumulation) must stay within
+# these of the fp64 oracle. The decode kernels keep P as a 16-bit hi + lo
+# pair: 1e-4. The row-block kernel (single-split launches with 64-row tiles:
+# prefill, wide verify) keeps P in fp16 with the V scale folded in, the
+# reference's precision class (11 significant bits: relative error up to
+# 2^-12 per term): BASELINE's own 2e-3, the arithmetic alone.
 F32_MAX_ABS = 1e-4
+F32_MAX_ABS_ROWS = 2e-3
+
+
+def row_block_launch(c: Case, S: int) -> bool:
+    """Whether the launcher takes the row-block kernel (attn_launch.hip:
+    D = 128, one split, pages of a multiple of 16 keys, bq * G >= 64)."""
+    plan = c.plan()
+    bq = tile_tokens(plan.wm, c.G, max(c.q_lens))
+    return c.D == 128 and S == 1 and c.block_size % 16 == 0 and bq * c.G >= 64
 
 
 def check_case(c: Case, *, num_splits=None, out_dtype=None, threads=16, strict=False):
@@ -107,8 +120,11 @@ def check_case(c: Case, *, num_splits=None, out_dtype=None, threads=16, strict=F
     # The same launch with fp32 output: the arithmetic alone.
     out32, _ = run_capi(b, num_splits=num_splits, out_dtype=torch.float32)
     r32 = compare(out32, None, ref_out, ref_lse, valid)
-    print(f"  fp32 out -> max abs {r32['max_abs']:.3g} mean abs {r32['mean_abs']:.3g}", flush=True)
-    assert r32["max_abs"] <= F32_MAX_ABS, f"{c.name}: fp32 max abs {r32['max_abs']:.3g}"
+    S = c.plan().num_splits if num_splits is None else num_splits
+    gate = F32_MAX_ABS_ROWS if row_block_launch(c, S) else F32_MAX_ABS
+    print(f"  fp32 out -> max abs {r32['max_abs']:.3g} mean abs {r32['mean_abs']:.3g} "
+          f"(gate {gate:g})", flush=True)
+    assert r32["max_abs"] <= gate, f"{c.name}: fp32 max abs {r32['max_abs']:.3g}"
     return b, out, lse
 
 

@@ -5,7 +5,8 @@
   so to fp32 accumulation error).
 * GPU: the HIP path reproduces every vector through the C ABI, with the
   planner's split count and unsplit, to the parity tolerance on bf16 output
-  (beyond bf16 storage rounding) and to 1e-4 on fp32 output.
+  (beyond bf16 storage rounding) and to 1e-4 on fp32 output (2e-3 for the
+  row-block kernel's launches, whose P is fp16).
 """
 
 from __future__ import annotations
@@ -104,7 +105,12 @@ def test_hip_reproduces_golden(name, split):
         o = out.float().cpu().numpy()[valid].astype(np.float64)
         err = np.abs(o - ref)
         if dtype == torch.float32:
-            assert err.max() <= 1e-4, f"{name}: fp32 max abs {err.max():.3g}"
+            # Row-block launches keep P in fp16 (the reference's precision
+            # class): BASELINE's 2e-3 on the arithmetic alone; 1e-4 otherwise.
+            rows_kernel = (D == 128 and S == 1 and g["k_cache"].shape[1] % 16 == 0
+                           and plan.bq * G >= 64)
+            gate = 2e-3 if rows_kernel else 1e-4
+            assert err.max() <= gate, f"{name}: fp32 max abs {err.max():.3g}"
         else:
             ex = np.maximum(err - half_ulp(ref, dtype), 0)
             assert ex.max() <= MAX_ABS and ex.mean() <= MEAN_ABS, (name, ex.max(), ex.mean())
