@@ -213,6 +213,36 @@ def test_row_blocks(case):
     check_case(case, num_splits=1)
 
 
+@pytest.mark.parametrize("big", [2.0 ** 12, 2.0 ** 40])
+def test_row_blocks_large_v_scales(big):
+    """The row-block kernel's fp16 P folds the V scales in under a running
+    exponent C: V scales far beyond fp16's range (V values up to 127 * 2^40),
+    growing mid-stream (keys [100, 200) scaled by `big`, keys [400, 410) by
+    big^2 in the second request), must neither overflow nor lose the small
+    rows' precision. Checked relative to each row's largest output."""
+    c = Case("rows-bigv", q_lens=[96, 70], seq_lens=[300, 620], seed=70)
+    assert row_block_launch(c, 1)
+    b = materialize(c, DEV)
+    ch = b.cache
+    bt = ch.block_table.cpu()
+    for r, (lo, hi, f) in enumerate([(100, 200, big), (400, 410, big * big)]):
+        for t in range(lo, min(hi, c.seq_lens[r])):
+            blk, slot = int(bt[r, t // c.block_size]), t % c.block_size
+            ch.v_scale[blk, slot] *= f
+    torch.cuda.synchronize()
+    ref_out, ref_lse, valid = oracle_of(b)
+    out32, lse = run_capi(b, num_splits=1, out_dtype=torch.float32)
+    o = out32.cpu().numpy()[valid].astype(np.float64)
+    r = ref_out[valid]
+    rowmax = np.abs(r).max(axis=-1, keepdims=True)
+    rel = np.abs(o - r) / rowmax
+    print(f"  big={big:g}: max rel {rel.max():.3g}, rows {valid.sum()}", flush=True)
+    assert np.isfinite(o).all()
+    assert rel.max() <= 2e-3, rel.max()
+    le = np.abs(lse.cpu().numpy()[valid] - ref_lse[valid])
+    assert le.max() <= 1e-3, le.max()
+
+
 def test_row_blocks_deterministic_and_op():
     c = Case("rows-op", q_lens=[100, 1, 9], seq_lens=[2000, 5000, 300], seed=64,
              num_splits=1)
