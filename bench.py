@@ -528,6 +528,75 @@ def measure_config(config: int, query_tokens: int, steps: int, warmup: int, cpu_
 ALL_CONFIGS = ((1, 1), (2, 1), (3, 1), (3, 4), (4, 1), (5, 1))
 
 
+def xcd_spread(steps: int, warmup: int, cus: int) -> dict:
+    """Finishing times of the page-row attention kernel by XCD on config 2:
+    the kernel as bench_hip/build.py builds it with PA_WAVE_CLOCK (each wave
+    records its XCD and its start and end time, s_memrealtime at 100 MHz),
+    launched alone through the C ABI like the kernel-alone loop of
+    measure_config; per launch, every time relative to the launch's first
+    wave start; reported as medians over `steps` launches."""
+    import ctypes
+    import statistics
+
+    import numpy as np
+    import torch
+
+    from pth_flash_attn import capi, planner
+    from pth_flash_attn.cache import build_cache, make_queries
+
+    lib = capi.AttnLib(REPO / "bench_hip" / "libpth_attn_clock.so")
+    read = lib.lib.pth_attn_debug_wave_clock
+    read.restype = ctypes.c_int32
+    read.argtypes = [ctypes.c_void_p, ctypes.c_int64]
+    name, q_lens, seq_lens, Hq, Hkv, window, is_prefill = workload(2)
+    G, D = Hq // Hkv, 128
+    cache = build_cache(seq_lens, Hkv=Hkv, D=D, block_size=16, seed=2, device="cuda:0")
+    q, qsl = make_queries(q_lens, Hq=Hq, D=D, seed=102, device="cuda:0")
+    T, R = len(q), len(q_lens)
+    ws_ts = planner.workspace_token_splits(max_num_seqs=R, q_dec_max=1, Hkv=Hkv, D=D, num_sms=cus)
+    plan = planner.plan_launch(num_tokens=T, num_reqs=R, max_query_len=1, G=G, Hkv=Hkv, D=D,
+                               num_sms=cus, is_prefill=False, ws_token_splits=max(ws_ts, T))
+    S = plan.num_splits
+    out = torch.empty_like(q)
+    ws_o = torch.empty(plan.ws_o_shape, device="cuda:0")
+    ws_lse = torch.empty(plan.ws_lse_shape, device="cuda:0")
+    args = capi.attn_args(q=q, out=out, k_cache=cache.k_cache, v_cache=cache.v_cache,
+                          k_scale=cache.k_scale, v_scale=cache.v_scale,
+                          block_table=cache.block_table, seq_lens=cache.seq_lens,
+                          query_start_loc=qsl, bq=1, num_splits=S,
+                          softmax_scale=1.0 / math.sqrt(D), ws_o=ws_o, ws_lse=ws_lse)
+    sp = torch.cuda.current_stream().cuda_stream
+    waves = cus * 8
+    buf = np.zeros(waves * 3, dtype=np.uint64)
+    for _ in range(max(warmup, 10)):
+        lib.check(lib.attention_kernel(args, sp))
+    torch.cuda.synchronize()
+    per_xcd_mean, per_xcd_p10, per_xcd_p90, last = {}, {}, {}, []
+    for _ in range(steps):
+        lib.check(lib.attention_kernel(args, sp))
+        torch.cuda.synchronize()
+        if read(buf.ctypes.data, waves) != 0:
+            raise RuntimeError("pth_attn_debug_wave_clock failed")
+        x = buf.reshape(waves, 3).astype(np.int64)
+        xcd, t0 = x[:, 0], x[:, 1].min()
+        end = (x[:, 2] - t0) / 100.0  # µs
+        last.append(float(end.max()))
+        for k in np.unique(xcd):
+            e = end[xcd == k]
+            per_xcd_mean.setdefault(int(k), []).append(float(e.mean()))
+            per_xcd_p10.setdefault(int(k), []).append(float(np.percentile(e, 10)))
+            per_xcd_p90.setdefault(int(k), []).append(float(np.percentile(e, 90)))
+    med = statistics.median
+    return {
+        "workload": name, "kernel": "attn_fwd_pagerows", "launches": steps, "waves": waves,
+        "last_wave_end_us": round(med(last), 1),
+        "by_xcd": {k: {"mean_end_us": round(med(v), 1),
+                       "p10_end_us": round(med(per_xcd_p10[k]), 1),
+                       "p90_end_us": round(med(per_xcd_p90[k]), 1)}
+                   for k, v in sorted(per_xcd_mean.items())},
+    }
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -543,6 +612,9 @@ def main() -> int:
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--reference-row", choices=sorted(REFERENCE_ROWS),
                     help="time one of the reference's published rows instead of a config")
+    ap.add_argument("--xcd-spread", action="store_true",
+                    help="only report config 2's page-row kernel finishing times by XCD "
+                         "(needs bench_hip/libpth_attn_clock.so, built by bench_hip/build.py)")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="only run a plain device copy of this many MiB, --steps times "
                          "(the reference point that scales rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -573,6 +645,9 @@ def main() -> int:
         print(json.dumps(reference_row(a.reference_row, a.steps * 4, a.warmup)))
         return 0
     cus = torch.cuda.get_device_properties(0).multi_processor_count
+    if a.xcd_spread:
+        print(json.dumps(xcd_spread(a.steps, a.warmup, cus)))
+        return 0
     threads = 0 if a.no_cpu else (a.cpu_threads or min(16, os.cpu_count() or 1))
     t_start = time.perf_counter()
     head = measure_config(a.config, a.query_tokens, a.steps, a.warmup, threads, cus,

@@ -234,6 +234,9 @@ void attn_fwd_staged(const AttnParams p) {
 // buffers, one being written while the other is read; rows padded to
 // kRowPad bytes so the head-strided operand reads spread over the banks)
 // and each wave computes its own head from it. One barrier per chunk.
+#ifdef PA_WAVE_CLOCK
+constexpr int kMaxClockWaves = 8192;
+#endif
 constexpr int kRowBytes = 2112;                      // 8 cells of 264 bytes
 constexpr int kRowPad = kRowBytes + 16;              // LDS bytes per key row
 constexpr int kRowBuf = kChunkTokens * kRowPad;      // one chunk buffer
@@ -309,10 +312,24 @@ __device__ __forceinline__ void rows_read(const char* buf, const AttnParams& p, 
   ch.sc = *reinterpret_cast<const float*>(cell + key * kRowPad + (r16 < 8 ? p.cell_off[2] : p.cell_off[3]));
 }
 
+#ifdef PA_WAVE_CLOCK
+// Measurement build only (bench_hip/build.py): per wave of the page-row
+// kernel, its XCD, start and end time (s_memrealtime, 100 MHz), so the
+// benchmark can report the finishing-time spread by XCD.
+__device__ uint64_t wave_clock[kMaxClockWaves * 3];
+// The XCD a wave runs on: hardware register XCC_ID, bits [3:0].
+__device__ __forceinline__ uint32_t xcc_id() {
+  return static_cast<uint32_t>(__builtin_amdgcn_s_getreg((3 << 11) | 20)) & 0xf;
+}
+#endif
+
 template <bool kWindow, bool kStream, bool kF16Q>
 __global__ __launch_bounds__(kFwdWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void attn_fwd_pagerows(const AttnParams p) {
   __shared__ __attribute__((aligned(16))) char lds_rows[2 * kRowBuf];
+#ifdef PA_WAVE_CLOCK
+  const uint64_t clock_start = __builtin_amdgcn_s_memrealtime();
+#endif
   const int lane = threadIdx.x & 63;
   const int L = threadIdx.x;
   const float scl = scale_factor(lane & 15, p.scale_log2);
@@ -348,6 +365,14 @@ void attn_fwd_pagerows(const AttnParams p) {
     }
     epilogue(p, U, Ls, st);
   }
+#ifdef PA_WAVE_CLOCK
+  const int w = static_cast<int>(blockIdx.x) * kFwdWaves + (static_cast<int>(threadIdx.x) >> 6);
+  if (lane == 0 && w < kMaxClockWaves) {
+    wave_clock[3 * w] = xcc_id();
+    wave_clock[3 * w + 1] = clock_start;
+    wave_clock[3 * w + 2] = __builtin_amdgcn_s_memrealtime();
+  }
+#endif
 }
 }  // namespace
 
@@ -381,3 +406,15 @@ hipError_t launch_staged_kernel(const AttnParams& p, dim3 grid, bool windowed, b
 }
 
 }  // namespace pa
+
+#ifdef PA_WAVE_CLOCK
+// Copies the last page-row launch's wave clock (XCD, start, end per wave;
+// waves of work-groups beyond the grid hold stale values) to host memory.
+extern "C" int32_t pth_attn_debug_wave_clock(uint64_t* dst, int64_t waves) {
+  const int64_t n = waves < pa::kMaxClockWaves ? waves : pa::kMaxClockWaves;
+  return hipMemcpyFromSymbol(dst, HIP_SYMBOL(pa::wave_clock), n * 3 * sizeof(uint64_t)) ==
+                 hipSuccess
+             ? 0
+             : -1;
+}
+#endif
