@@ -351,7 +351,9 @@ __device__ __forceinline__ void compute_rows(const RowSet& R, const Lanes (&L)[2
       for (int e = 0; e < 4; ++e)
         t[i][4 * sub + e] = fmaf(acc[i][e], ks[4 * sub + e], -m_use[i]);
   }
-  __builtin_amdgcn_s_setprio(0);
+  // Waves 4-7 keep priority 1 for the whole block (see attn_fwd_rows).
+  if ((__builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x)) >> 8) == 0)
+    __builtin_amdgcn_s_setprio(0);
   ops.load_v();
   if (c < R.w_lo_max || c + kChunkTokens - 1 > R.w_hi_min) {
     // Keys outside a row's range get p = 0; keys outside every row's range
@@ -827,6 +829,13 @@ void attn_fwd_rows(const AttnParams p) {
   while (walk.next(p, lane, B)) {
     // The previous block's merge reads of the slots are done.
     __syncthreads();
+    // Waves w and w + 4 share a SIMD, and between two barriers the arbiter's
+    // preference for the older wave let waves 0-3 finish each step 0.5-0.8 us
+    // before waves 4-7 and wait for them at the next barrier (per-step
+    // timestamps, config 5's prefill part). Waves 4-7 therefore run the whole
+    // block at priority 1, waves 0-3 only during their QK products
+    // (compute_rows): the prefill part 4.05 -> 3.97 ms.
+    if (wave >= kRowWaves / 2) __builtin_amdgcn_s_setprio(1);
     const int mask = (1 << B.log_rs) - 1;
     const int rs = wave & mask;
     const int part = wave >> B.log_rs;
