@@ -528,13 +528,15 @@ def measure_config(config: int, query_tokens: int, steps: int, warmup: int, cpu_
 ALL_CONFIGS = ((1, 1), (2, 1), (3, 1), (3, 4), (4, 1), (5, 1))
 
 
-def xcd_spread(steps: int, warmup: int, cus: int) -> dict:
-    """Finishing times of the page-row attention kernel by XCD on config 2:
-    the kernel as bench_hip/build.py builds it with PA_WAVE_CLOCK (each wave
-    records its XCD and its start and end time, s_memrealtime at 100 MHz),
-    launched alone through the C ABI like the kernel-alone loop of
-    measure_config; per launch, every time relative to the launch's first
-    wave start; reported as medians over `steps` launches."""
+def xcd_spread(steps: int, warmup: int, cus: int, config: int = 2, query_tokens: int = 1) -> dict:
+    """Start and finishing times of the page-row attention kernel by XCD on a
+    configuration it runs (2 or 3): the kernel as bench_hip/build.py builds it
+    with PA_WAVE_CLOCK (each wave records its XCD and its start and end time,
+    s_memrealtime at 100 MHz), launched alone through the C ABI like the
+    kernel-alone loop of measure_config; per launch, every time relative to
+    the launch's first wave start; reported as medians over `steps`
+    launches. Records left by waves of earlier launches (slots beyond this
+    grid) are those that started more than 30 µs before the last start."""
     import ctypes
     import statistics
 
@@ -548,39 +550,54 @@ def xcd_spread(steps: int, warmup: int, cus: int) -> dict:
     read = lib.lib.pth_attn_debug_wave_clock
     read.restype = ctypes.c_int32
     read.argtypes = [ctypes.c_void_p, ctypes.c_int64]
-    name, q_lens, seq_lens, Hq, Hkv, window, is_prefill = workload(2)
+    name, q_lens, seq_lens, Hq, Hkv, window, is_prefill = workload(config, query_tokens)
     G, D = Hq // Hkv, 128
-    cache = build_cache(seq_lens, Hkv=Hkv, D=D, block_size=16, seed=2, device="cuda:0")
-    q, qsl = make_queries(q_lens, Hq=Hq, D=D, seed=102, device="cuda:0")
-    T, R = len(q), len(q_lens)
-    ws_ts = planner.workspace_token_splits(max_num_seqs=R, q_dec_max=1, Hkv=Hkv, D=D, num_sms=cus)
-    plan = planner.plan_launch(num_tokens=T, num_reqs=R, max_query_len=1, G=G, Hkv=Hkv, D=D,
-                               num_sms=cus, is_prefill=False, ws_token_splits=max(ws_ts, T))
+    cache = build_cache(seq_lens, Hkv=Hkv, D=D, block_size=16, seed=config, device="cuda:0")
+    q, qsl = make_queries(q_lens, Hq=Hq, D=D, seed=config + 100, device="cuda:0")
+    T, R, q_max = len(q), len(q_lens), max(q_lens)
+    ws_ts = planner.workspace_token_splits(max_num_seqs=R, q_dec_max=q_max, Hkv=Hkv, D=D, num_sms=cus)
+    plan = planner.plan_launch(num_tokens=T, num_reqs=R, max_query_len=q_max, G=G, Hkv=Hkv, D=D,
+                               num_sms=cus, is_prefill=is_prefill, ws_token_splits=max(ws_ts, T),
+                               window=window)
     S = plan.num_splits
+    # The op's row-tile height (csrc/torch_op.cpp tile_tokens).
+    cap = 16 * plan.wm // G
+    bq = q_max if 1 <= q_max < cap and planner.wm_for_rows(q_max * G) == plan.wm else cap
     out = torch.empty_like(q)
     ws_o = torch.empty(plan.ws_o_shape, device="cuda:0")
     ws_lse = torch.empty(plan.ws_lse_shape, device="cuda:0")
     args = capi.attn_args(q=q, out=out, k_cache=cache.k_cache, v_cache=cache.v_cache,
                           k_scale=cache.k_scale, v_scale=cache.v_scale,
                           block_table=cache.block_table, seq_lens=cache.seq_lens,
-                          query_start_loc=qsl, bq=1, num_splits=S,
-                          softmax_scale=1.0 / math.sqrt(D), ws_o=ws_o, ws_lse=ws_lse)
+                          query_start_loc=qsl, bq=bq, num_splits=S,
+                          softmax_scale=1.0 / math.sqrt(D), ws_o=ws_o, ws_lse=ws_lse,
+                          window=window)
     sp = torch.cuda.current_stream().cuda_stream
-    waves = cus * 8
+    waves = 8192
     buf = np.zeros(waves * 3, dtype=np.uint64)
     for _ in range(max(warmup, 10)):
         lib.check(lib.attention_kernel(args, sp))
     torch.cuda.synchronize()
     per_xcd_mean, per_xcd_p10, per_xcd_p90, last = {}, {}, {}, []
+    overall = {k: [] for k in ("start_p50", "start_p90", "start_max", "end_p10", "end_p50", "end_p90")}
+    counted = []
     for _ in range(steps):
         lib.check(lib.attention_kernel(args, sp))
         torch.cuda.synchronize()
         if read(buf.ctypes.data, waves) != 0:
             raise RuntimeError("pth_attn_debug_wave_clock failed")
         x = buf.reshape(waves, 3).astype(np.int64)
+        x = x[x[:, 1] >= x[:, 1].max() - 3000]
         xcd, t0 = x[:, 0], x[:, 1].min()
-        end = (x[:, 2] - t0) / 100.0  # µs
+        start = (x[:, 1] - t0) / 100.0  # µs
+        end = (x[:, 2] - t0) / 100.0
+        counted.append(len(x))
         last.append(float(end.max()))
+        overall["start_p50"].append(float(np.percentile(start, 50)))
+        overall["start_p90"].append(float(np.percentile(start, 90)))
+        overall["start_max"].append(float(start.max()))
+        for q_, k_ in ((10, "end_p10"), (50, "end_p50"), (90, "end_p90")):
+            overall[k_].append(float(np.percentile(end, q_)))
         for k in np.unique(xcd):
             e = end[xcd == k]
             per_xcd_mean.setdefault(int(k), []).append(float(e.mean()))
@@ -588,8 +605,10 @@ def xcd_spread(steps: int, warmup: int, cus: int) -> dict:
             per_xcd_p90.setdefault(int(k), []).append(float(np.percentile(e, 90)))
     med = statistics.median
     return {
-        "workload": name, "kernel": "attn_fwd_pagerows", "launches": steps, "waves": waves,
+        "workload": name, "kernel": "attn_fwd_pagerows", "launches": steps,
+        "waves": int(med(counted)), "num_splits": S,
         "last_wave_end_us": round(med(last), 1),
+        "all_waves_us": {k: round(med(v), 1) for k, v in overall.items()},
         "by_xcd": {k: {"mean_end_us": round(med(v), 1),
                        "p10_end_us": round(med(per_xcd_p10[k]), 1),
                        "p90_end_us": round(med(per_xcd_p90[k]), 1)}
@@ -613,7 +632,8 @@ def main() -> int:
     ap.add_argument("--reference-row", choices=sorted(REFERENCE_ROWS),
                     help="time one of the reference's published rows instead of a config")
     ap.add_argument("--xcd-spread", action="store_true",
-                    help="only report config 2's page-row kernel finishing times by XCD "
+                    help="only report the page-row kernel's start and finishing times by XCD "
+                         "on --config (2 or 3) "
                          "(needs bench_hip/libpth_attn_clock.so, built by bench_hip/build.py)")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="only run a plain device copy of this many MiB, --steps times "
@@ -646,7 +666,7 @@ def main() -> int:
         return 0
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     if a.xcd_spread:
-        print(json.dumps(xcd_spread(a.steps, a.warmup, cus)))
+        print(json.dumps(xcd_spread(a.steps, a.warmup, cus, a.config, a.query_tokens)))
         return 0
     threads = 0 if a.no_cpu else (a.cpu_threads or min(16, os.cpu_count() or 1))
     t_start = time.perf_counter()
