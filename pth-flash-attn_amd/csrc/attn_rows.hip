@@ -126,10 +126,19 @@ __device__ __forceinline__ void make_block(const AttnParams& p, const RowTile& t
 // The blocks of one work-group, in order (a prefix sum over requests, 64 per
 // wave instruction, as the unit table of attn_fwd.hip). Within each group of
 // 64 requests the requests are taken in decreasing order of their estimated
-// work (row tiles x keys per row): the work-groups start on the long blocks
-// and the short ones fill the end, which evens out their finishing times
-// (a mixed prefill + decode batch whose long decodes came last left some
-// work-groups a decode block behind the others).
+// work (row tiles x keys per row), so that the snake of rounds (work-group b
+// takes unit b of even rounds and W - 1 - b of odd ones) pairs long blocks
+// with short ones and evens out the work-groups' totals (a mixed prefill +
+// decode batch whose long decodes came last left some work-groups a decode
+// block behind the others).
+//
+// Each work-group walks its rounds starting at round b mod R (R rounds in
+// all) and wraps around: the same blocks, in a rotated order. In a mixed
+// batch the decode blocks (HBM-bound, ranked last) then run at different
+// times on different compute units, beside other units' prefill blocks
+// (MFMA-bound), instead of all at the end, where every unit streamed decode
+// keys at once and HBM bounded them (config 5: 4.84 ms, the sum of its
+// prefill part alone, 3.95 ms, and its decode part alone, 0.89 ms).
 template <bool kWindow>
 struct BlockWalk {
   int r0 = -64;
@@ -137,43 +146,80 @@ struct BlockWalk {
   int incl = 0;
   int sreq = 0;  // lane k: the request (within the group) of rank k
   int round = 0;
+  int total = -1;  // units of the launch (-1: not counted yet)
+  int nrounds = 0;
+  int rot = 0;     // the work-group's first round
+
+  // Moves to the next group of 64 requests: their ranks and the prefix sum
+  // of their units. False past the last request.
+  __device__ __forceinline__ bool scan_group(const AttnParams& p, int lane) {
+    r0 += 64;
+    u0 = u1;
+    if (r0 >= p.num_reqs) return false;
+    const int r = r0 + lane;
+    int tiles = 0;
+    float work = -1.0f;  // lanes past the last request sort last
+    if (r < p.num_reqs) {
+      const int q_len = p.qsl[r + 1] - p.qsl[r];
+      tiles = request_row_tiles(q_len, p.blk_tok);
+      work = static_cast<float>(tiles) * static_cast<float>(p.seq_lens[r] - q_len / 2);
+    }
+    // Rank: requests with more work first, ties in request order.
+    int rank = 0;
+    for (int j = 0; j < 64; ++j) {
+      const float wj =
+          __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, work), j));
+      rank += (wj > work || (wj == work && j < lane)) ? 1 : 0;
+    }
+    sreq = __builtin_amdgcn_ds_permute(rank * 4, lane);
+    const int units = __builtin_amdgcn_ds_permute(rank * 4, tiles * p.num_kv_heads);
+    int x = units;
+#pragma unroll
+    for (int dd = 1; dd < 64; dd <<= 1) {
+      const int v = __shfl_up(x, dd);
+      if (lane >= dd) x += v;
+    }
+    incl = x;
+    u1 = u0 + __builtin_amdgcn_readlane(x, 63);
+    return true;
+  }
+
+  // Units of the whole launch: the first group's prefix sum when it holds
+  // every request, else a count over all requests.
+  __device__ __forceinline__ int count_units(const AttnParams& p, int lane) {
+    if (p.num_reqs <= 64) return scan_group(p, lane) ? u1 : 0;
+    int n = 0;
+    for (int g = 0; g < p.num_reqs; g += 64) {
+      const int r = g + lane;
+      int tiles = r < p.num_reqs ? request_row_tiles(p.qsl[r + 1] - p.qsl[r], p.blk_tok) : 0;
+#pragma unroll
+      for (int dd = 32; dd >= 1; dd >>= 1) tiles += __shfl_xor(tiles, dd);
+      n += __builtin_amdgcn_readfirstlane(tiles);
+    }
+    return n * p.num_kv_heads;
+  }
 
   __device__ __forceinline__ bool next(const AttnParams& p, int lane, Block& B) {
     const int W = gridDim.x;
     const int b = blockIdx.x;
-    const int u = round * W + ((round & 1) ? W - 1 - b : b);
-    ++round;
-    while (u >= u1) {
-      r0 += 64;
-      u0 = u1;
-      if (r0 >= p.num_reqs) return false;
-      const int r = r0 + lane;
-      int tiles = 0;
-      float work = -1.0f;  // lanes past the last request sort last
-      if (r < p.num_reqs) {
-        const int q_len = p.qsl[r + 1] - p.qsl[r];
-        tiles = request_row_tiles(q_len, p.blk_tok);
-        work = static_cast<float>(tiles) *
-               static_cast<float>(p.seq_lens[r] - q_len / 2);
-      }
-      // Rank: requests with more work first, ties in request order.
-      int rank = 0;
-      for (int j = 0; j < 64; ++j) {
-        const float wj = __builtin_bit_cast(
-            float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, work), j));
-        rank += (wj > work || (wj == work && j < lane)) ? 1 : 0;
-      }
-      sreq = __builtin_amdgcn_ds_permute(rank * 4, lane);
-      const int units = __builtin_amdgcn_ds_permute(rank * 4, tiles * p.num_kv_heads);
-      int x = units;
-#pragma unroll
-      for (int dd = 1; dd < 64; dd <<= 1) {
-        const int v = __shfl_up(x, dd);
-        if (lane >= dd) x += v;
-      }
-      incl = x;
-      u1 = u0 + __builtin_amdgcn_readlane(x, 63);
+    if (total < 0) {
+      total = count_units(p, lane);
+      nrounds = (total + W - 1) / W;
+      rot = nrounds > 1 ? b % nrounds : 0;
     }
+    int u;
+    do {
+      if (round >= nrounds) return false;
+      const int rr = round + rot < nrounds ? round + rot : round + rot - nrounds;
+      ++round;
+      u = rr * W + ((rr & 1) ? W - 1 - b : b);
+    } while (u >= total);
+    if (u < u0) {  // a wrapped round: scan again from the first group
+      r0 = -64;
+      u0 = u1 = 0;
+    }
+    while (u >= u1)
+      if (!scan_group(p, lane)) return false;
     const int local = u - u0;
     const int j = static_cast<int>(__popcll(__ballot(incl <= local)));
     const int req = r0 + __builtin_amdgcn_readlane(sreq, j);
