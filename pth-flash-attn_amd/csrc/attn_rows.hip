@@ -132,8 +132,10 @@ __device__ __forceinline__ void make_block(const AttnParams& p, const RowTile& t
 // decode batch whose long decodes came last left some work-groups a decode
 // block behind the others).
 //
-// Each work-group walks its rounds starting at round b mod R (R rounds in
-// all) and wraps around: the same blocks, in a rotated order. In a mixed
+// Each work-group walks its rounds starting at round (b / H) mod R (R
+// rounds in all, H KV heads) and wraps around: the same blocks, in a rotated
+// order, the H work-groups that take the H KV heads of a row tile in the
+// same round (adjacent heads' cells share cache lines). In a mixed
 // batch the decode blocks (HBM-bound, ranked last) then run at different
 // times on different compute units, beside other units' prefill blocks
 // (MFMA-bound), instead of all at the end, where every unit streamed decode
@@ -205,7 +207,7 @@ struct BlockWalk {
     if (total < 0) {
       total = count_units(p, lane);
       nrounds = (total + W - 1) / W;
-      rot = nrounds > 1 ? b % nrounds : 0;
+      rot = nrounds > 1 ? (b / p.num_kv_heads) % nrounds : 0;
     }
     int u;
     do {
@@ -305,21 +307,83 @@ __device__ __forceinline__ void row_loader(const AttnParams& p, const Block& B, 
   Ld.bt0 = static_cast<int64_t>(B.t.req) * p.bt_stride;
 }
 
-// Pages of the chunk at key c (scalar loads). A 16-key group outside the
-// block's keys reads page 0 (masked later).
+// Block-table windows of a key part (the parts path): each wave keeps 64
+// consecutive entries of its request's block-table row, from block
+// wb0 + 64 w, in LDS (two buffers: window w and w + 1), loaded with one
+// direct-to-LDS dword load per lane. A chunk's pages are then two LDS reads,
+// where a scalar load of the block table per chunk left every chunk step
+// waiting for the previous step's load (decode blocks: 2 of 3 us per step).
+// Window w + 1 is loaded when window w comes into use, at least 32 chunks
+// (64 blocks of >= 16 keys) before its first use: the chunk waits in between
+// (vmcnt, in-order completion) cover its load. The extra loads only make
+// those waits count one operation too few, that is wait longer, never less.
+constexpr int kBtWindow = 64;                          // entries per window
+constexpr int kBtWaveBytes = 2 * kBtWindow * 4;        // two windows per wave
+constexpr int kBtBase = kRowSlots * kSlotBytes;        // after the chunk slots
+constexpr int kRowLds = kBtBase + kRowWaves * kBtWaveBytes;
+static_assert(kRowLds <= 160 * 1024, "row-block kernel LDS");
+
+struct BtWindows {
+  int wb0;       // first block of window 0
+  int wi;        // the current window
+  int last_blk;  // last block a load may read (inside the request's row)
+};
+
+// Window w of the wave's buffers `bt` (lane l: entry min(wb0 + 64 w + l,
+// last_blk) of the row).
+__device__ __forceinline__ void bt_window_load(const AttnParams& p, const RowLoader& Ld,
+                                               const BtWindows& W, int w, char* bt, int lane) {
+  int e = W.wb0 + kBtWindow * w + lane;
+  e = e < W.last_blk ? e : W.last_blk;
+  dma4(reinterpret_cast<const char*>(p.block_table + Ld.bt0 + e), bt + (w & 1) * (kBtWindow * 4));
+}
+
+// Windows 0 and 1 of a part whose keys start at c0 (issued before the
+// vmcnt(0) that waits for the query).
+__device__ __forceinline__ void bt_windows_start(const AttnParams& p, const Block& B,
+                                                 const RowLoader& Ld, int c0, BtWindows& W,
+                                                 char* bt, int lane) {
+  const int first = c0 > B.ld_lo ? c0 : B.ld_lo;
+  W.wb0 = static_cast<int>(p.bs_div.div(first));
+  W.wi = 0;
+  W.last_blk = static_cast<int>(p.bs_div.div(B.ld_hi > 0 ? B.ld_hi - 1 : 0));
+  bt_window_load(p, Ld, W, 0, bt, lane);
+  bt_window_load(p, Ld, W, 1, bt, lane);
+}
+
+// Pages of the chunk at key c from the windows (a 16-key group outside the
+// block's keys gets page 0, masked later). Blocks only move forward, so a
+// block past window wi + 1 never occurs before window wi + 1 is current.
 __device__ __forceinline__ void rows_pages(const AttnParams& p, const Block& B, int c,
-                                           RowLoader& Ld) {
+                                           RowLoader& Ld, BtWindows& W, char* bt,
+                                           uint32_t bt_lds, int lane) {
+  bool use[2];
+  int blk[2];
 #pragma unroll
   for (int sub = 0; sub < 2; ++sub) {
     const int c16 = c + 16 * sub;
-    Ld.page[sub] = 0;
-    Ld.slot0[sub] = 0;
-    if (c16 < B.ld_hi && c16 + 16 > B.ld_lo) {
-      const int blk = static_cast<int>(p.bs_div.div(c16));
-      Ld.slot0[sub] = c16 - blk * static_cast<int>(p.bs_div.d);
-      Ld.page[sub] = ld_ro(p.block_table, Ld.bt0 + blk);
+    use[sub] = c16 < B.ld_hi && c16 + 16 > B.ld_lo;
+    blk[sub] = use[sub] ? static_cast<int>(p.bs_div.div(c16)) : W.wb0;
+    Ld.slot0[sub] = use[sub] ? c16 - blk[sub] * static_cast<int>(p.bs_div.d) : 0;
+  }
+  const int b0 = use[0] ? blk[0] : blk[1];
+  if (use[0] || use[1]) {
+    const int need = (b0 - W.wb0) >> 6;
+    if (need > W.wi) {  // window wi + 1 becomes current; load wi + 2
+      ++W.wi;
+      bt_window_load(p, Ld, W, W.wi + 1, bt, lane);
     }
   }
+  float e[2];
+#pragma unroll
+  for (int sub = 0; sub < 2; ++sub) {
+    const int d = blk[sub] - W.wb0;
+    e[sub] = ds_read4(bt_lds + (((d >> 6) & 1) * kBtWindow + (d & 63)) * 4);
+  }
+  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(e[0]), "+v"(e[1]) : : "memory");
+#pragma unroll
+  for (int sub = 0; sub < 2; ++sub)
+    Ld.page[sub] = use[sub] ? __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, e[sub])) : 0;
 }
 
 // This wave's share of the 9 loads of the chunk whose pages Ld holds: loads
@@ -863,7 +927,7 @@ __device__ __forceinline__ void wide_block(const AttnParams& p, const Block& B, 
 template <bool kWindow, bool kF16Q>
 __global__ __launch_bounds__(kRowWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void attn_fwd_rows(const AttnParams p) {
-  __shared__ __attribute__((aligned(16))) char lds[kRowSlots * kSlotBytes];
+  __shared__ __attribute__((aligned(16))) char lds[kRowLds];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t lds_base = lds_offset(lds);
@@ -907,6 +971,13 @@ void attn_fwd_rows(const AttnParams p) {
     Lanes L[2];
     L[0] = unit_lanes<kWindow>(p, U0, lane);
     L[1] = R.two ? unit_lanes<kWindow>(p, U1, lane) : L[0];
+    RowLoader Ld;
+    row_loader(p, B, lane, Ld);
+    const int c0 = B.c_begin + kChunkTokens * pc0;
+    char* bt = lds + kBtBase + wave * kBtWaveBytes;
+    const uint32_t bt_lds = lds_base + kBtBase + wave * kBtWaveBytes;
+    BtWindows btw;
+    if (kp > 1 && len > 0) bt_windows_start(p, B, Ld, c0, btw, bt, lane);
     bf16x8 qb[2][4], qlo[2][4];
     if (R.has_rows) {
       load_q<kF16Q>(p, L[0], qb[0], qlo[0]);
@@ -920,15 +991,13 @@ void attn_fwd_rows(const AttnParams p) {
         }
       }
     }
-    // Q has landed (a compiler-visible vmcnt(0): the chunk waits below are
-    // asm the compiler does not see).
+    // Q (and the block-table windows) have landed (a compiler-visible
+    // vmcnt(0): the chunk waits below are asm the compiler does not see).
     __builtin_amdgcn_s_waitcnt(0x0F70);
     State st[2];
     state_reset(st[0]);
     state_reset(st[1]);
 
-    RowLoader Ld;
-    row_loader(p, B, lane, Ld);
     if (kp == 1) {
       wide_block<kF16Q>(p, B, R, L, Ld, qb, qlo, scl, st, lds, lds_base, ro, cvo, wave, lane);
       if (R.has_rows) {
@@ -937,11 +1006,10 @@ void attn_fwd_rows(const AttnParams p) {
       }
       continue;
     }
-    const int c0 = B.c_begin + kChunkTokens * pc0;
-    if (len > 0) rows_pages(p, B, c0, Ld);
+    if (len > 0) rows_pages(p, B, c0, Ld, btw, bt, bt_lds, lane);
     for (int i = 0; i < ahead && i < len; ++i) {
       issue_rows_chunk(p, Ld, ring + i * kSlotBytes, rs, mask, lane);
-      if (i + 1 < len) rows_pages(p, B, c0 + kChunkTokens * (i + 1), Ld);
+      if (i + 1 < len) rows_pages(p, B, c0 + kChunkTokens * (i + 1), Ld, btw, bt, bt_lds, lane);
     }
     const int nsteps = solo ? len : steps;
     int vexp = kNoExp;
@@ -957,12 +1025,13 @@ void attn_fwd_rows(const AttnParams p) {
       const int c = c0 + kChunkTokens * k;
       const bool mine = k < len && R.has_rows && c <= R.w_hi_max && c + kChunkTokens > R.w_lo_min;
       Chunk ch;
-      // Read before the issue below: its page lookup shares the LDS reads'
-      // wait counter.
+      // Read before the issue below: its page lookup waits for the LDS
+      // counter.
       if (mine) read_chunk(ring_base + (k % ns) * kSlotBytes, ro, ch);
       if (k + ahead < len) {
         issue_rows_chunk(p, Ld, ring + ((k + ahead) % ns) * kSlotBytes, rs, mask, lane);
-        if (k + ahead + 1 < len) rows_pages(p, B, c + kChunkTokens * (ahead + 1), Ld);
+        if (k + ahead + 1 < len)
+          rows_pages(p, B, c + kChunkTokens * (ahead + 1), Ld, btw, bt, bt_lds, lane);
       }
       if (mine) {
         Int8Ops ops{ch};
