@@ -204,17 +204,23 @@ struct BlockWalk {
   __device__ __forceinline__ bool next(const AttnParams& p, int lane, Block& B) {
     const int W = gridDim.x;
     const int b = blockIdx.x;
+    const int H = p.num_kv_heads;
+    const int M = W % H == 0 ? W / H : 0;
+    // The work-group's slot in every round: slot H t + h (KV head h of the
+    // round's t-th row tile) is work-group h M + t, so the H heads of a row
+    // tile run on work-groups congruent modulo 8, that is on one XCD.
+    const int slot = M > 0 ? (b % M) * H + b / M : b;
     if (total < 0) {
       total = count_units(p, lane);
       nrounds = (total + W - 1) / W;
-      rot = nrounds > 1 ? (b / p.num_kv_heads) % nrounds : 0;
+      rot = nrounds > 1 ? (slot / H) % nrounds : 0;
     }
     int u;
     do {
       if (round >= nrounds) return false;
       const int rr = round + rot < nrounds ? round + rot : round + rot - nrounds;
       ++round;
-      u = rr * W + ((rr & 1) ? W - 1 - b : b);
+      u = rr * W + ((rr & 1) ? W - 1 - slot : slot);
     } while (u >= total);
     if (u < u0) {  // a wrapped round: scan again from the first group
       r0 = -64;
