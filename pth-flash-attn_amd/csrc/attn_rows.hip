@@ -30,9 +30,10 @@
 //
 // Work order. Blocks are (request, token block, KV head), KV head fastest,
 // the requests of each group of 64 in decreasing order of estimated work, the
-// token blocks of a request from its last (longest key range) to its first;
-// work-group b of W takes block b of each round of W blocks, in reversed
-// order on odd rounds, so long and short blocks pair up.
+// token blocks of a request from its last (longest key range) to its first,
+// dealt in rounds of W blocks (snake order, so long and short blocks pair
+// up; the KV heads of a token block to work-groups on one XCD); each
+// work-group walks its rounds from a rotated start (see BlockWalk).
 
 #include "attn_device.h"
 
