@@ -205,6 +205,15 @@ GRID_ROWS = [
          q_lens=[40, 1, 0, 70] + [1] * 60 + [33] + [1] * 35,
          seq_lens=[300, 500, 7, 70] + [200 + 40 * (i % 7) for i in range(60)] + [900]
                   + [650] * 20 + [64 + 97 * i for i in range(15)], Hq=8, Hkv=2, seed=65),
+    # More blocks than work-groups and more than 64 requests: the walk counts
+    # the blocks over both request groups, every work-group starts at a
+    # rotated round and wraps around (scanning the groups again), and the 8
+    # KV heads of a row tile go to work-groups of one XCD.
+    Case("rows-many-requests-rounds",
+         q_lens=[1] * 90 + [20, 65, 130, 1, 0, 3, 40, 1, 9, 70],
+         seq_lens=[100 + 37 * (i % 11) for i in range(90)]
+                  + [400, 65, 900, 2000, 5, 3, 300, 1, 1200, 70],
+         Hq=32, Hkv=8, seed=66),
 ]
 
 
