@@ -163,6 +163,12 @@ __device__ __forceinline__ void dma4(const char* g, char* lds) {
       (const void __attribute__((address_space(1)))*)(g),
       (void __attribute__((address_space(3)))*)(lds), 4, 0, 0);
 }
+// A global load with the non-temporal hint (cache policy nt): for cache
+// bytes that the launch reads once and no other wave reads.
+template <class T>
+__device__ __forceinline__ T ld_nt(const char* g) {
+  return __builtin_nontemporal_load(reinterpret_cast<const T*>(g));
+}
 
 // K/V rows in a slot are 128 bytes; their 16-byte pieces are stored in the
 // order piece ^ (key & 7), so the reads below (8 keys at the same piece per

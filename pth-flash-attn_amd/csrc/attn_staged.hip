@@ -252,6 +252,11 @@ struct RowStaged {
   uint32_t tail;
 };
 
+// The loads carry the non-temporal hint: every cache line of the chunk is
+// fetched by exactly one wave and never again in the launch (config 2:
+// 364.5 -> 350.4 us). The kernels whose waves share lines (neighbouring
+// heads' cells, the row groups of a KV head) keep ordinary loads: the hint
+// there cost config 4 39.6 -> 63.0 us and config 5 4.56 -> 4.81 ms.
 __device__ __forceinline__ void rows_load(const AttnParams& p, const ChunkPages& cp, int L,
                                           RowStaged& S) {
   const char* base[2];
@@ -265,9 +270,9 @@ __device__ __forceinline__ void rows_load(const AttnParams& p, const ChunkPages&
     const int i = L + 512 * j;
     const int grp = i >= kPiecesPerGroup ? 1 : 0;  // j < 4: 0; j > 4: 1
     const int w = i - grp * kPiecesPerGroup;
-    S.piece[j] = *reinterpret_cast<const u32x4*>((grp ? base[1] : base[0]) + 16 * w);
+    S.piece[j] = ld_nt<u32x4>((grp ? base[1] : base[0]) + 16 * w);
   }
-  S.tail = *reinterpret_cast<const uint32_t*>(base[1] + (65536 - kGroupBytes) + 4 * L);
+  S.tail = ld_nt<uint32_t>(base[1] + (65536 - kGroupBytes) + 4 * L);
 }
 
 __device__ __forceinline__ void rows_write(char* buf, int L, const RowStaged& S) {
