@@ -235,7 +235,7 @@ def read_ceiling(cache, seq_lens, cus: int, reps: int = 10) -> dict:
     return {"value": round(gbs, 1), "unit": "GB/s", "frac_of_peak": round(gbs / PEAK_HBM_GBS, 4),
             "bytes": byts, "us": round(ms * 1e3, 2),
             "what": "bench_hip/ceilings.hip read_groups: config 2's cache bytes, whole slot rows "
-                    "in 16-byte register loads, two 16-key groups in flight per work-group, "
+                    "in 16-byte non-temporal register loads, two 16-key groups in flight per work-group, "
                     f"one work-group per CU, mean of {reps} launches"}
 
 

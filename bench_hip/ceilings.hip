@@ -8,8 +8,8 @@
 //    launch -- for each (page, slots) entry the first `slots` slot rows of
 //    one 16-slot group of a page -- with the attention kernel's load
 //    pattern (work-groups of 512 lanes, whole slot rows in 16-byte register
-//    loads, two groups in flight per work-group, static equal ranges of
-//    entries per work-group) and discards them. Its GB/s is the achievable
+//    loads with the non-temporal hint, two groups in flight per work-group,
+//    static equal ranges of entries per work-group) and discards them. Its GB/s is the achievable
 //    read rate of that byte set.
 //  * pth_bench_mfma: back-to-back v_mfma_f32_16x16x32_bf16 on 8 waves per CU
 //    (2 per SIMD, the row-block kernel's occupancy), 8 independent
@@ -53,7 +53,8 @@ __global__ __launch_bounds__(512) void read_groups(const char* base, int64_t pag
 #pragma unroll
       for (int j = 0; j < 5; ++j) {
         const int i = L + 512 * j;
-        v[h][j] = i < n ? *reinterpret_cast<const u32x4*>(src + 16 * i) : (u32x4){0, 0, 0, 0};
+        v[h][j] = i < n ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + 16 * i))
+                        : (u32x4){0, 0, 0, 0};
       }
     }
 #pragma unroll
