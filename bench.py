@@ -641,7 +641,8 @@ def main() -> int:
     a = ap.parse_args()
     if a.gpus != 1:
         print("bench.py measures one GPU: this path runs on one device (the op has no "
-              "multi-GPU form; sharding is by KV head or request, see DESIGN.md). "
+              "multi-GPU form; a multi-GPU deployment shards the KV heads or the requests "
+              "and runs one launch per GPU on its shard). "
               "Run with --gpus 1.", file=sys.stderr)
         return 2
 
