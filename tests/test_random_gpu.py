@@ -55,3 +55,30 @@ def test_random_batch(seed):
     print(f"random case {seed}: D={c.D} G={c.G} Hkv={c.Hkv} layout={c.layout} "
           f"q_dtype={c.q_dtype} S={S}", flush=True)
     check_case(c, num_splits=S, threads=16)
+
+
+def random_rows_case(seed: int) -> Case:
+    """A prefill-style batch of 65-100 requests on the row-block kernel
+    (num_splits = 1, 64-row tiles): more requests than one group of 64 in the
+    block walk and, with 8 KV heads, more blocks than work-groups, so the
+    walk's rotated rounds wrap and its request groups are scanned again."""
+    rng = random.Random(50_000 + seed)
+    R = rng.randint(65, 100)
+    Hkv = rng.choice([2, 4, 8, 8])
+    G = rng.choice([1, 2, 4, 4, 8])
+    q_lens = [rng.choice([1, 1, 1, 2, 5, 17, 40, 70, 130]) for _ in range(R)]
+    q_lens[rng.randrange(R)] = 0  # a request without query tokens
+    seq_lens = [q + rng.randint(0, 600) for q in q_lens]
+    window = rng.choice([0, 0, 0, 64, 300])
+    return Case(f"rand-rows{seed}", q_lens=q_lens, seq_lens=seq_lens, Hq=G * Hkv, Hkv=Hkv,
+                block_size=rng.choice([16, 32, 64]), window=window,
+                q_dtype=rng.choice([torch.bfloat16, torch.float16]), is_prefill=True,
+                seed=2000 + seed)
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_random_row_blocks_many_requests(seed):
+    c = random_rows_case(seed)
+    print(f"random rows case {seed}: R={len(c.q_lens)} G={c.G} Hkv={c.Hkv} W={c.window} "
+          f"q_dtype={c.q_dtype}", flush=True)
+    check_case(c, num_splits=1, threads=16)
