@@ -203,13 +203,19 @@ __device__ __forceinline__ void prod256_offsets(const AttnParams& p, const Unit&
 
 __device__ __forceinline__ void prod256_pages(const AttnParams& p, const Unit& U, int c,
                                               Prod256& P) {
-  const int64_t bt0 = static_cast<int64_t>(U.t.req) * p.bt_stride;
+  // The unit is wave-uniform; saying so makes the block-table reads scalar
+  // loads (lgkmcnt), which never wait for the chunk loads in flight.
+  const int req = __builtin_amdgcn_readfirstlane(U.t.req);
+  const int ld_lo = __builtin_amdgcn_readfirstlane(U.ld_lo);
+  const int ld_hi = __builtin_amdgcn_readfirstlane(U.ld_hi);
+  c = __builtin_amdgcn_readfirstlane(c);
+  const int64_t bt0 = static_cast<int64_t>(req) * p.bt_stride;
 #pragma unroll
   for (int sub = 0; sub < 2; ++sub) {
     const int c16 = c + 16 * sub;
     P.page[sub] = 0;
     P.slot0[sub] = 0;
-    if (c16 < U.ld_hi && c16 + 16 > U.ld_lo) {
+    if (c16 < ld_hi && c16 + 16 > ld_lo) {
       const int blk = static_cast<int>(p.bs_div.div(c16));
       P.slot0[sub] = c16 - blk * static_cast<int>(p.bs_div.d);
       P.page[sub] = ld_ro(p.block_table, bt0 + blk);
