@@ -133,10 +133,11 @@ __device__ __forceinline__ void make_block(const AttnParams& p, const RowTile& t
 // decode batch whose long decodes came last left some work-groups a decode
 // block behind the others).
 //
-// Each work-group walks its rounds starting at round (b / H) mod R (R
-// rounds in all, H KV heads) and wraps around: the same blocks, in a rotated
-// order, the H work-groups that take the H KV heads of a row tile in the
-// same round (adjacent heads' cells share cache lines). In a mixed
+// Each work-group walks its rounds starting at round t mod R (R rounds in
+// all; t = b mod (W / H), its row-tile slot, H KV heads) and wraps around:
+// the same blocks, in a rotated order, the H work-groups that take the H KV
+// heads of a row tile in the same round (adjacent heads' cells share cache
+// lines). In a mixed
 // batch the decode blocks (HBM-bound, ranked last) then run at different
 // times on different compute units, beside other units' prefill blocks
 // (MFMA-bound), instead of all at the end, where every unit streamed decode
@@ -208,8 +209,9 @@ struct BlockWalk {
     const int H = p.num_kv_heads;
     const int M = W % H == 0 ? W / H : 0;
     // The work-group's slot in every round: slot H t + h (KV head h of the
-    // round's t-th row tile) is work-group h M + t, so the H heads of a row
-    // tile run on work-groups congruent modulo 8, that is on one XCD.
+    // round's t-th row tile) is work-group h M + t (M = W / H). Work-groups
+    // are dealt to the 8 XCDs in turn, so with M a multiple of 8 (a full
+    // grid of 256) the H heads of a row tile run on one XCD.
     const int slot = M > 0 ? (b % M) * H + b / M : b;
     if (total < 0) {
       total = count_units(p, lane);
