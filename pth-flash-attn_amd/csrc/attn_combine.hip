@@ -193,10 +193,39 @@ __device__ __forceinline__ void merge_blocks(const CombineParams& c, int64_t tok
 // or past S drop it. Same arithmetic in the same order as merge_blocks, so
 // the results are identical; the partial rows are issued kOB at a time.
 template <int NC, int kBlk>
+constexpr int kOneBatch = kBatch<NC> < kBlk ? kBatch<NC> : kBlk;
+
+// The partial rows of splits kBlk first + k, k < kSpec (at most the first
+// batch merge_one_block merges), loaded before the split count is known:
+// every slot below num_splits is workspace memory, and a row whose split
+// turns out to have no weight (past the count, or -inf) never enters an
+// arithmetic operation. kSpec trades the round trip saved against the rows
+// read for nothing: few for many rows with few live splits each, the whole
+// batch for few rows with many.
+template <int NC, int kBlk, int kSpec>
+__device__ __forceinline__ void spec_rows(const CombineParams& c, int64_t tok, int head,
+                                          int first, int lane, float (&ov)[kSpec][NC]) {
+  static_assert(kSpec >= 1 && kSpec <= kOneBatch<NC, kBlk>, "speculative rows: the first batch");
+  const char* o_row =
+      c.ws_o + tok * c.s_wo_tok + static_cast<int64_t>(head) * c.s_wo_head + 4 * NC * lane;
+#pragma unroll
+  for (int k = 0; k < kSpec; ++k) {
+    const int s = kBlk * first + k;
+    if (s < c.num_splits) {
+      load_cols<NC>(o_row + static_cast<int64_t>(s) * c.s_wo_split, ov[k]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < NC; ++i) ov[k][i] = 0.0f;
+    }
+  }
+}
+
+template <int NC, int kBlk, int kSpec>
 __device__ __forceinline__ void merge_one_block(const CombineParams& c, int64_t tok, int head,
-                                                int S, int first, float x_spec, int lane,
+                                                int S, int first, float x_spec,
+                                                const float (&ov_spec)[kSpec][NC], int lane,
                                                 float& M, float (&num)[NC], float& den) {
-  constexpr int kOB = kBatch<NC> < kBlk ? kBatch<NC> : kBlk;
+  constexpr int kOB = kOneBatch<NC, kBlk>;
   const char* o_row =
       c.ws_o + tok * c.s_wo_tok + static_cast<int64_t>(head) * c.s_wo_head + 4 * NC * lane;
   const int s0 = kBlk * first;
@@ -217,7 +246,10 @@ __device__ __forceinline__ void merge_one_block(const CombineParams& c, int64_t 
       w[k] = e < n ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(
                                                     __builtin_bit_cast(int, w_l), e))
                    : 0.0f;
-      if (w[k] > 0.0f) {
+      if (e0 == 0 && k < kSpec) {  // loaded with the LSEs
+#pragma unroll
+        for (int i = 0; i < NC; ++i) ov[k][i] = ov_spec[k < kSpec ? k : 0][i];
+      } else if (w[k] > 0.0f) {
         load_cols<NC>(o_row + (s0 + e) * c.s_wo_split, ov[k]);
       } else {
 #pragma unroll
@@ -302,19 +334,22 @@ __global__ __launch_bounds__(256) void combine_splits(const CombineParams c) {
   const int64_t tok = row / c.num_q_heads;
   const int head = static_cast<int>(row - tok * c.num_q_heads);
   if (tok >= c.num_tokens) return;
-  // The marker, the padding bound and (when every split fits one 64-split
-  // block) the LSEs are loaded in one round.
-  const bool one_block = c.num_splits <= 64;
+  // The marker, the padding bound, the first 64 LSEs and the first batch of
+  // partial rows are loaded in one round; a row whose splits (the marker's
+  // count) fit one 64-split block is then merged without another LSE round.
   const int bound = ld_ro(c.qsl, c.num_reqs);
   const uint32_t bits = marker_bits(c, tok, head);  // read on every path: the slot exists
-  const float x_spec = one_block ? lse_slot<64>(c, tok, head, 0, lane) : kNegInf;
+  const float x_spec = lse_slot<64>(c, tok, head, 0, lane);
+  constexpr int kSpec = 4;  // many rows, few live splits each
+  float ov_spec[kSpec][NC];
+  spec_rows<NC, 64, kSpec>(c, tok, head, 0, lane, ov_spec);
   if (tok >= bound) return;  // padding row
   const int S = c.seq_lens != nullptr ? splits_of_marker(c, bits) : c.num_splits;
   if (c.seq_lens != nullptr && S == 1) return;  // written to out by the attention kernel
   float M, den;
   float num[NC];
-  if (one_block)
-    merge_one_block<NC, 64>(c, tok, head, S, 0, x_spec, lane, M, num, den);
+  if (S <= 64)
+    merge_one_block<NC, 64, kSpec>(c, tok, head, S, 0, x_spec, ov_spec, lane, M, num, den);
   else
     merge_blocks<NC>(c, tok, head, S, 0, 1, lane, M, num, den);
   write_row<NC>(c, tok, head, M, num, den, lane);
@@ -340,19 +375,23 @@ __global__ __launch_bounds__(kSharedWaves * 64) void combine_shared(const Combin
   const int64_t tok = row / c.num_q_heads;
   const int head = static_cast<int>(row - tok * c.num_q_heads);
   if (tok >= c.num_tokens) return;  // uniform over the work-group
-  // The padding bound, the marker and (when every split fits one block per
-  // wave) the wave's LSEs are loaded in one round.
-  const bool one_block = c.num_splits <= kSharedWaves * kSharedBlock;
+  // The padding bound, the marker, the wave's block of LSEs and its first
+  // batch of partial rows are loaded in one round; when the row's splits (the
+  // marker's count) fit one block per wave no further LSE round follows.
   const int bound = ld_ro(c.qsl, c.num_reqs);
   const uint32_t bits = marker_bits(c, tok, head);  // read on every path: the slot exists
-  const float x_spec = one_block ? lse_slot<kSharedBlock>(c, tok, head, wave, lane) : kNegInf;
+  const float x_spec = lse_slot<kSharedBlock>(c, tok, head, wave, lane);
+  constexpr int kSpec = kOneBatch<NC, kSharedBlock>;  // few rows, many splits each
+  float ov_spec[kSpec][NC];
+  spec_rows<NC, kSharedBlock, kSpec>(c, tok, head, wave, lane, ov_spec);
   if (tok >= bound) return;  // padding row, uniform over the work-group
   const int S = c.seq_lens != nullptr ? splits_of_marker(c, bits) : c.num_splits;
   if (c.seq_lens != nullptr && S == 1) return;  // written to out by the attention kernel
   float M, den;
   float num[NC];
-  if (one_block)
-    merge_one_block<NC, kSharedBlock>(c, tok, head, S, wave, x_spec, lane, M, num, den);
+  if (S <= kSharedWaves * kSharedBlock)
+    merge_one_block<NC, kSharedBlock, kSpec>(c, tok, head, S, wave, x_spec, ov_spec, lane, M,
+                                             num, den);
   else
     merge_blocks<NC, kSharedBlock>(c, tok, head, S, wave, kSharedWaves, lane, M, num, den);
   if (lane == 0) {
