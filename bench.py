@@ -13,15 +13,17 @@ Printed (one JSON line on stdout):
   value / ms_per_step  the headline layer call: algorithmic bytes / time over
                        exactly K eager steps after W warm-up steps (HIP events
                        on the launch stream, synchronised on both sides);
-  roofline             the attention kernel alone (HIP events over K launches
-                       on the launch stream), its algorithmic bytes per launch
+  roofline             the attention kernel: HIP events around it inside each of
+                       K layer calls (attention, event, combine) on the launch
+                       stream, right after the op's timed calls; its
+                       algorithmic bytes per launch
                        against MI355X's 8 TB/s, the HBM traffic per launch from
                        the committed rocprofv3 counter summary (or null), and
                        the measured read ceiling of the same bytes;
   configs              every BASELINE configuration (1, 2, 3 at 1 and 4 query
                        tokens, 4, 5): layer call (eager mean and the median of
-                       graph-replayed calls), attention and combine kernels
-                       timed alone, GB/s or TFLOP/s against the roofline, and
+                       graph-replayed calls, >= 200 launches), attention and
+                       combine kernels timed inside the calls, GB/s or TFLOP/s against the roofline, and
                        the CPU baseline. Inputs smaller than 1 GiB are rotated
                        over copies so that at least 1 GiB passes between two
                        reads of the same bytes (cold MALL);
@@ -59,6 +61,7 @@ METRIC = "µs/layer-call + achieved HBM GB/s (% peak), int8 paged decode D=128"
 
 # Untimed warm-up lasts at least this long (seconds of GPU work), W steps at least.
 WARMUP_MIN_S = 0.3
+GRAPH_REPLAYS = 10  # x 20 layer calls per replay: the median covers 200 launches
 
 def workload(config: int, query_tokens: int = 1):
     """(name, q_lens, seq_lens, Hq, Hkv, window, is_prefill) of a BASELINE config.
@@ -388,6 +391,27 @@ def _events_ms(stream, n, fn) -> float:
     return e0.elapsed_time(e1) / n
 
 
+def _kernel_events_ms(stream, n, first, second=None) -> tuple[float, float | None]:
+    """Mean ms of first(i) and of second(i) over n calls of first(i); second(i),
+    each kernel bracketed by HIP events on `stream` (synchronised)."""
+    import torch
+
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(3 * n)]
+    torch.cuda.synchronize()
+    for i in range(n):
+        ev[3 * i].record(stream)
+        first(i)
+        ev[3 * i + 1].record(stream)
+        if second is not None:
+            second(i)
+            ev[3 * i + 2].record(stream)
+    torch.cuda.synchronize()
+    a = sum(ev[3 * i].elapsed_time(ev[3 * i + 1]) for i in range(n)) / n
+    if second is None:
+        return a, None
+    return a, sum(ev[3 * i + 1].elapsed_time(ev[3 * i + 2]) for i in range(n)) / n
+
+
 def measure_config(config: int, query_tokens: int, steps: int, warmup: int, cpu_threads: int,
                    cus: int, graph: bool = True, keep_inputs: bool = False) -> dict:
     """One BASELINE configuration through the op: see the module docstring."""
@@ -441,8 +465,30 @@ def measure_config(config: int, query_tokens: int, steps: int, warmup: int, cpu_
     ms = _events_ms(stream, steps, step)
     wall = time.perf_counter() - t0
 
+    # The two kernels of the layer call, each timed inside the call: the same
+    # K layer calls through the C ABI, launched exactly as the op launches
+    # them, with an event before the attention kernel, one between it and the
+    # combine and one after, all on the launch stream. Run right after the op's
+    # timed calls, so both see the same clocks; attention + combine is then
+    # the whole call, and the attention average is what the roofline uses.
+    lib = capi.AttnLib()
+    bq = 16 * plan.wm // G
+    if 1 <= q_max < bq and planner.wm_for_rows(q_max * G) == plan.wm:
+        bq = q_max
+    arg_sets = [capi.attn_args(q=qq, out=out, k_cache=c.k_cache, v_cache=c.v_cache,
+                               k_scale=c.k_scale, v_scale=c.v_scale, block_table=c.block_table,
+                               seq_lens=c.seq_lens, query_start_loc=ql, bq=bq, num_splits=S,
+                               softmax_scale=scale, ws_o=ws_o, ws_lse=ws_lse, window=window)
+                for c, qq, ql in sets]
+    sp = stream.cuda_stream
+    attn_ms, comb_ms = _kernel_events_ms(
+        stream, steps,
+        lambda i: lib.check(lib.attention_kernel(arg_sets[i % copies], sp)),
+        (lambda i: lib.check(lib.combine_kernel(arg_sets[i % copies], sp))) if S > 1 else None)
+
     # The same layer calls replayed from a captured graph (the reference times
-    # graph-replayed launches): the median over replays of 20 calls each.
+    # graph-replayed launches): the median over GRAPH_REPLAYS replays of 20 calls each
+    # (at least 200 launches).
     graph_us = None
     if graph:
         per_graph = 20
@@ -461,7 +507,7 @@ def measure_config(config: int, query_tokens: int, steps: int, warmup: int, cpu_
         torch.cuda.synchronize()
         reps = []
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        for _ in range(max(5, min(30, 2 * steps // per_graph))):
+        for _ in range(GRAPH_REPLAYS):
             e0.record(stream)
             g.replay()
             e1.record(stream)
@@ -469,23 +515,6 @@ def measure_config(config: int, query_tokens: int, steps: int, warmup: int, cpu_
             reps.append(e0.elapsed_time(e1) / per_graph)
         graph_us = statistics.median(reps) * 1e3
         del g
-
-    # The two kernels of a layer call alone, through the C ABI exactly as the
-    # op launches them, on the same stream.
-    lib = capi.AttnLib()
-    bq = 16 * plan.wm // G
-    if 1 <= q_max < bq and planner.wm_for_rows(q_max * G) == plan.wm:
-        bq = q_max
-    arg_sets = [capi.attn_args(q=qq, out=out, k_cache=c.k_cache, v_cache=c.v_cache,
-                               k_scale=c.k_scale, v_scale=c.v_scale, block_table=c.block_table,
-                               seq_lens=c.seq_lens, query_start_loc=ql, bq=bq, num_splits=S,
-                               softmax_scale=scale, ws_o=ws_o, ws_lse=ws_lse, window=window)
-                for c, qq, ql in sets]
-    sp = stream.cuda_stream
-    attn_ms = _events_ms(stream, steps, lambda i: lib.check(lib.attention_kernel(arg_sets[i % copies], sp)))
-    comb_ms = None
-    if S > 1:
-        comb_ms = _events_ms(stream, steps, lambda i: lib.check(lib.combine_kernel(arg_sets[0], sp)))
 
     byts, attn_bytes, flops = algorithmic(q_lens, seq_lens, Hq, Hkv, window)
     res = {
@@ -515,6 +544,14 @@ def measure_config(config: int, query_tokens: int, steps: int, warmup: int, cpu_
                            "algorithmic_bytes": attn_bytes,
                            "traffic": profile_traffic("attn_fwd_d128", name)}
     res["pct_of_peak_hbm"] = round(100.0 * res["gbs"] / PEAK_HBM_GBS, 2)
+    if graph_us is not None:
+        # The whole layer call (attention + combine) at its graph-replayed median.
+        if is_prefill:
+            res["roofline"]["frac_layer_call_graph_median"] = round(
+                flops / (graph_us * 1e-6) / 1e12 / PEAK_BF16_TFLOPS, 4)
+        else:
+            res["roofline"]["frac_layer_call_graph_median"] = round(
+                byts / (graph_us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4)
     if cpu_threads > 0:
         res["cpu_baseline"] = cpu_baseline(cache, q, qsl, q_lens, seq_lens, Hq, Hkv, window,
                                            cpu_threads)

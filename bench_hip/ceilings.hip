@@ -93,18 +93,24 @@ float time_launches(int reps, hipStream_t stream, Launch launch, hipError_t* err
   *err = hipEventCreate(&e0);
   if (*err != hipSuccess) return -1.f;
   *err = hipEventCreate(&e1);
-  if (*err != hipSuccess) return -1.f;
-  launch();  // untimed
-  hipEventRecord(e0, stream);
-  for (int i = 0; i < reps; ++i) launch();
-  hipEventRecord(e1, stream);
-  *err = hipEventSynchronize(e1);
+  if (*err != hipSuccess) {
+    hipEventDestroy(e0);
+    return -1.f;
+  }
   float ms = 0.f;
+  launch();  // untimed
+  *err = hipGetLastError();
+  if (*err == hipSuccess) *err = hipEventRecord(e0, stream);
+  if (*err == hipSuccess) {
+    for (int i = 0; i < reps; ++i) launch();
+    *err = hipGetLastError();
+  }
+  if (*err == hipSuccess) *err = hipEventRecord(e1, stream);
+  if (*err == hipSuccess) *err = hipEventSynchronize(e1);
   if (*err == hipSuccess) *err = hipEventElapsedTime(&ms, e0, e1);
-  if (*err == hipSuccess) *err = hipGetLastError();
   hipEventDestroy(e0);
   hipEventDestroy(e1);
-  return ms / reps;
+  return *err == hipSuccess ? ms / reps : -1.f;
 }
 
 }  // namespace

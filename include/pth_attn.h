@@ -245,7 +245,9 @@ int32_t pth_attn_combine_kernel(const PthAttnArgs* args, void* stream);
 
 /* pth_attn_attention_lse with no allocation and no workspace argument: the
  * split partials live in a static device array of the library (64 MiB per
- * GPU, held from the first call on a device until the process ends) instead
+ * GPU, reserved when the library's code object loads onto a device, for every
+ * user of the library whether or not it calls this entry, and held until the
+ * process ends; its address is looked up on the first call) instead
  * of args->ws_o / args->ws_lse, which are ignored. lse may be NULL (then
  * this is the op's layer call: attention + combine into args->out). Rejects
  * with EINVAL, before any launch, a batch whose partials need more than the

@@ -187,11 +187,7 @@ __device__ __forceinline__ void merge_blocks(const CombineParams& c, int64_t tok
   den = wave_sum(den_l);
 }
 
-// Merge of block `first` alone (every split of the row lies in the wave's
-// one block), with the block's log2-LSEs already loaded: x_spec is lane l's
-// slot kBlk first + l, read before the split count S was known, so lanes at
-// or past S drop it. Same arithmetic in the same order as merge_blocks, so
-// the results are identical; the partial rows are issued kOB at a time.
+// Partial rows merge_one_block issues per batch: a load batch, at most a block.
 template <int NC, int kBlk>
 constexpr int kOneBatch = kBatch<NC> < kBlk ? kBatch<NC> : kBlk;
 
@@ -220,6 +216,11 @@ __device__ __forceinline__ void spec_rows(const CombineParams& c, int64_t tok, i
   }
 }
 
+// Merge of block `first` alone (every split of the row lies in the wave's
+// one block), with the block's log2-LSEs already loaded: x_spec is lane l's
+// slot kBlk first + l, read before the split count S was known, so lanes at
+// or past S drop it. Same arithmetic in the same order as merge_blocks, so
+// the results are identical; the partial rows are issued kOB at a time.
 template <int NC, int kBlk, int kSpec>
 __device__ __forceinline__ void merge_one_block(const CombineParams& c, int64_t tok, int head,
                                                 int S, int first, float x_spec,

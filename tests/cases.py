@@ -123,6 +123,15 @@ def oracle_of(b: Batch, *, threads: int = 0) -> tuple[np.ndarray, np.ndarray, np
     return oracle.attention(args, threads=threads)
 
 
+def abs_v_batch(b: Batch) -> Batch:
+    """A host copy of the batch whose V values are |V| (every int8 the writer
+    produces lies in [-127, 127], so the absolute value is exact): the oracle
+    on it gives sum_i p_i |v_id| / l per output element."""
+    hc = b.cache.to("cpu")
+    hc.v_cache.abs_()
+    return Batch(b.case, hc, b.q.cpu(), b.qsl.cpu())
+
+
 def half_ulp(ref: np.ndarray, dtype: torch.dtype) -> np.ndarray:
     """Half an ulp of ``ref`` in the output dtype: the rounding any exact kernel
     incurs when it stores ``ref`` (bf16: 8 significant bits, fp16: 11)."""

@@ -19,7 +19,7 @@ import pytest
 import torch
 
 from cases import (
-    Case, Batch, assert_parity, compare, launch_args, materialize, oracle_of,
+    Case, Batch, abs_v_batch, assert_parity, compare, launch_args, materialize, oracle_of,
     tile_tokens, uniform_lengths,
 )
 
@@ -88,12 +88,37 @@ def run_op(b: Batch, *, num_splits: int | None = None):
 # fp32 outputs carry no storage rounding: the kernel's own arithmetic (exact
 # int8 K/V and q in bf16, fp32 scores, fp32 accumulation) must stay within
 # these of the fp64 oracle. The decode kernels keep P as a 16-bit hi + lo
-# pair: 1e-4. The row-block kernel (single-split launches with 64-row tiles:
-# prefill, wide verify) keeps P in fp16 with the V scale folded in, the
-# reference's precision class (11 significant bits: relative error up to
-# 2^-12 per term): BASELINE's own 2e-3, the arithmetic alone.
+# pair: 1e-4 everywhere.
 F32_MAX_ABS = 1e-4
-F32_MAX_ABS_ROWS = 2e-3
+# The row-block kernel (single-split launches with 64-row tiles: prefill,
+# wide verify) keeps P in fp16 with the V scale folded in, the reference's
+# precision class: each term p_i v_i of a row's sum carries one fp16 rounding
+# (relative error <= 2^-11, 11 significant bits), every other operation is
+# fp32. So element d of a row is within 2^-11 (sum_i p_i |v_id|) / l of the
+# exact value, plus fp32 noise: the oracle run on |V| gives that sum
+# exactly, and every element must meet the bound (F32_ROWS_SLACK covers the
+# fp32 part). The bound takes every rounding at its largest, u = 2^-11 of its
+# term; round-to-nearest errs by u/2 on average (|delta| uniform on [0, u]), so
+# the mean error over a launch is at most half the mean bound in expectation,
+# which F32_ROWS_MEAN_RATIO gates (a kernel whose rounding error doubled
+# would exceed it; random row-block launches measure 0.2-0.37).
+F32_ROWS_UNIT = 2.0 ** -11
+F32_ROWS_SLACK = 2e-5
+F32_ROWS_MEAN_RATIO = 0.5
+
+
+def fp32_row_block_gate(b: Batch, out32: torch.Tensor, ref_out: np.ndarray,
+                        valid: np.ndarray, *, threads: int = 16) -> dict:
+    """The row-block kernel's fp32-output check (see F32_ROWS_UNIT): returns
+    the worst element's error over its bound and the mean-error ratio."""
+    ab = abs_v_batch(b)
+    abs_out, _, _ = oracle_of(ab, threads=threads)
+    bound = F32_ROWS_UNIT * abs_out[valid] + F32_ROWS_SLACK
+    err = np.abs(out32.float().cpu().numpy()[valid].astype(np.float64) - ref_out[valid])
+    return {"max_over_bound": float((err / bound).max()) if err.size else 0.0,
+            "mean_ratio": float(err.mean() / (F32_ROWS_UNIT * abs_out[valid]).mean())
+            if err.size else 0.0,
+            "max_abs": float(err.max()) if err.size else 0.0}
 
 
 def row_block_launch(c: Case, S: int) -> bool:
@@ -121,10 +146,17 @@ def check_case(c: Case, *, num_splits=None, out_dtype=None, threads=16, strict=F
     out32, _ = run_capi(b, num_splits=num_splits, out_dtype=torch.float32)
     r32 = compare(out32, None, ref_out, ref_lse, valid)
     S = c.plan().num_splits if num_splits is None else num_splits
-    gate = F32_MAX_ABS_ROWS if row_block_launch(c, S) else F32_MAX_ABS
-    print(f"  fp32 out -> max abs {r32['max_abs']:.3g} mean abs {r32['mean_abs']:.3g} "
-          f"(gate {gate:g})", flush=True)
-    assert r32["max_abs"] <= gate, f"{c.name}: fp32 max abs {r32['max_abs']:.3g}"
+    if row_block_launch(c, S):
+        g = fp32_row_block_gate(b, out32, ref_out, valid, threads=threads)
+        print(f"  fp32 out (row blocks) -> max abs {g['max_abs']:.3g} mean abs "
+              f"{r32['mean_abs']:.3g}, worst error / bound {g['max_over_bound']:.3g}, "
+              f"mean error / mean bound {g['mean_ratio']:.3g}", flush=True)
+        assert g["max_over_bound"] <= 1.0, f"{c.name}: fp32 error beyond the fp16-P bound ({g})"
+        assert g["mean_ratio"] <= F32_ROWS_MEAN_RATIO, f"{c.name}: fp32 mean error ({g})"
+    else:
+        print(f"  fp32 out -> max abs {r32['max_abs']:.3g} mean abs {r32['mean_abs']:.3g} "
+              f"(gate {F32_MAX_ABS:g})", flush=True)
+        assert r32["max_abs"] <= F32_MAX_ABS, f"{c.name}: fp32 max abs {r32['max_abs']:.3g}"
     return b, out, lse
 
 

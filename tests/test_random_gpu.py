@@ -6,7 +6,8 @@ GQA group, KV heads, head size, window and causality, block size, page
 layout, query dtype, forced split count) so that combinations nobody thought
 of meet the same gate: max abs <= 2e-3 and mean abs <= 2e-4 on the 16-bit
 output, |dLSE| <= 1e-3, and the same launch with fp32 output within 1e-4
-(2e-3 on row-block launches, whose P is fp16: test_attn_gpu.check_case).
+(on row-block launches, whose P is fp16, the fp16-P rounding bound of
+test_attn_gpu.fp32_row_block_gate).
 Sizes are kept small enough for the oracle to finish each case in well under
 a second. Every case prints its parameters before it runs.
 """

@@ -110,3 +110,83 @@ def test_noalloc_single_split_needs_no_scratch(lib):
     case = Case("noalloc-s1", q_lens=[1, 3], seq_lens=[1200, 400], seed=33)
     b, out_na, lse_na, out_ws, lse_ws, out_nl = _run_pair(lib, case, 1)
     assert torch.equal(out_na, out_ws) and torch.equal(out_nl, out_ws)
+
+
+def _capture_and_compare(lib, case: Case, S: int, *, warm: bool) -> None:
+    """Capture the noalloc layer call (with its LSE) in a torch CUDA graph,
+    replay it three times with eager work and synchronisations in between,
+    and compare every replay bit for bit with the workspace entry."""
+    print(f"noalloc capture {case.name}: S={S} warm={warm}", flush=True)
+    b = materialize(case, "cuda")
+    bq = case.plan().bq
+    T = b.q.shape[0]
+    out_g = torch.zeros_like(b.q)
+    lse_g = torch.zeros((T, case.Hq), device="cuda")
+    ws_o = torch.empty((S, T, case.Hq, case.D), device="cuda")
+    ws_l = torch.empty((S, T, case.Hq), device="cuda")
+    # The workspace only shapes the argument struct; the entry ignores it.
+    a_g = launch_args(b, out_g, num_splits=S, bq=bq, ws_o=ws_o, ws_lse=ws_l)
+    a_g.ws_o = None
+    a_g.ws_lse = None
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    if warm:
+        with torch.cuda.stream(stream):
+            lib.check(lib.attention_lse_noalloc(a_g, lse_g, stream.cuda_stream))
+        stream.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        lib.check(lib.attention_lse_noalloc(a_g, lse_g, stream.cuda_stream))
+    out_w = torch.empty_like(b.q)
+    lse_w = torch.full((T, case.Hq), float("nan"), device="cuda")
+    lib.check(lib.attention_lse(launch_args(b, out_w, num_splits=S, bq=bq, ws_o=ws_o,
+                                            ws_lse=ws_l), lse_w))
+    torch.cuda.synchronize()
+    valid = torch.from_numpy(oracle_of(b)[2]).to("cuda")
+    for i in range(3):
+        out_g.zero_()
+        lse_g.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out_g, out_w), f"{case.name}: replay {i} out"
+        assert torch.equal(lse_g[valid], lse_w[valid]), f"{case.name}: replay {i} lse"
+        # Eager work between replays: another noalloc call on a smaller batch.
+        other = torch.empty_like(b.q)
+        lib.check(lib.attention_lse_noalloc(launch_args(b, other, num_splits=2, bq=bq,
+                                                        ws_o=ws_o[:2], ws_lse=ws_l[:2])))
+        torch.cuda.synchronize()
+    del graph
+
+
+def capture_first_call_child() -> None:
+    """Run in a fresh process: the graph capture is the library's first
+    noalloc call, so the scratch address lookup happens inside the capture."""
+    lib = capi.AttnLib()
+    _capture_and_compare(lib, Case("noalloc-capture-first", q_lens=[1, 4, 1],
+                                   seq_lens=[5000, 2100, 333], seed=35), 24, warm=False)
+    print("capture-first OK", flush=True)
+
+
+@needs_lib
+@pytest.mark.gpu
+def test_noalloc_under_graph_capture_after_a_warm_call(lib):
+    _capture_and_compare(lib, Case("noalloc-capture-warm", q_lens=[1, 2, 1, 4],
+                                   seq_lens=[7000, 1500, 90, 4000], seed=34), 32, warm=True)
+
+
+@needs_lib
+@pytest.mark.gpu
+def test_noalloc_under_graph_capture_as_the_first_call():
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    here = Path(__file__).resolve().parent
+    code = ("import sys; sys.path[:0] = [%r, %r, %r]; import test_zz_no_alloc as t; "
+            "t.capture_first_call_child()" % (str(here), str(here.parent / "pth-flash-attn_amd"
+                                                           / "python"), str(here.parent)))
+    r = subprocess.run([sys.executable, "-u", "-c", code], capture_output=True, text=True,
+                       timeout=110)
+    print(r.stdout[-2000:], r.stderr[-2000:], flush=True)
+    assert r.returncode == 0 and "capture-first OK" in r.stdout
