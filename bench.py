@@ -13,17 +13,18 @@ Printed (one JSON line on stdout):
   value / ms_per_step  the headline layer call: algorithmic bytes / time over
                        exactly K eager steps after W warm-up steps (HIP events
                        on the launch stream, synchronised on both sides);
-  roofline             the attention kernel: HIP events around it inside each of
-                       K layer calls (attention, event, combine) on the launch
-                       stream, right after the op's timed calls; its
+  roofline             the attention kernel alone: the median of 5 blocks of K
+                       back-to-back launches (HIP events on the launch
+                       stream), interleaved with blocks of K layer calls; its
                        algorithmic bytes per launch
                        against MI355X's 8 TB/s, the HBM traffic per launch from
                        the committed rocprofv3 counter summary (or null), and
                        the measured read ceiling of the same bytes;
   configs              every BASELINE configuration (1, 2, 3 at 1 and 4 query
                        tokens, 4, 5): layer call (eager mean and the median of
-                       graph-replayed calls, >= 200 launches), attention and
-                       combine kernels timed inside the calls, GB/s or TFLOP/s against the roofline, and
+                       graph-replayed calls, >= 200 launches; the median of
+                       the interleaved blocks), attention and combine kernels
+                       alone (median of the interleaved blocks), GB/s or TFLOP/s against the roofline, and
                        the CPU baseline. Inputs smaller than 1 GiB are rotated
                        over copies so that at least 1 GiB passes between two
                        reads of the same bytes (cold MALL);
@@ -62,6 +63,7 @@ METRIC = "µs/layer-call + achieved HBM GB/s (% peak), int8 paged decode D=128"
 # Untimed warm-up lasts at least this long (seconds of GPU work), W steps at least.
 WARMUP_MIN_S = 0.3
 GRAPH_REPLAYS = 10  # x 20 layer calls per replay: the median covers 200 launches
+KERNEL_BLOCKS = 5  # interleaved blocks of K launches for the per-kernel medians
 
 def workload(config: int, query_tokens: int = 1):
     """(name, q_lens, seq_lens, Hq, Hkv, window, is_prefill) of a BASELINE config.
@@ -391,27 +393,6 @@ def _events_ms(stream, n, fn) -> float:
     return e0.elapsed_time(e1) / n
 
 
-def _kernel_events_ms(stream, n, first, second=None) -> tuple[float, float | None]:
-    """Mean ms of first(i) and of second(i) over n calls of first(i); second(i),
-    each kernel bracketed by HIP events on `stream` (synchronised)."""
-    import torch
-
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(3 * n)]
-    torch.cuda.synchronize()
-    for i in range(n):
-        ev[3 * i].record(stream)
-        first(i)
-        ev[3 * i + 1].record(stream)
-        if second is not None:
-            second(i)
-            ev[3 * i + 2].record(stream)
-    torch.cuda.synchronize()
-    a = sum(ev[3 * i].elapsed_time(ev[3 * i + 1]) for i in range(n)) / n
-    if second is None:
-        return a, None
-    return a, sum(ev[3 * i + 1].elapsed_time(ev[3 * i + 2]) for i in range(n)) / n
-
-
 def measure_config(config: int, query_tokens: int, steps: int, warmup: int, cpu_threads: int,
                    cus: int, graph: bool = True, keep_inputs: bool = False) -> dict:
     """One BASELINE configuration through the op: see the module docstring."""
@@ -465,12 +446,14 @@ def measure_config(config: int, query_tokens: int, steps: int, warmup: int, cpu_
     ms = _events_ms(stream, steps, step)
     wall = time.perf_counter() - t0
 
-    # The two kernels of the layer call, each timed inside the call: the same
-    # K layer calls through the C ABI, launched exactly as the op launches
-    # them, with an event before the attention kernel, one between it and the
-    # combine and one after, all on the launch stream. Run right after the op's
-    # timed calls, so both see the same clocks; attention + combine is then
-    # the whole call, and the attention average is what the roofline uses.
+    # The two kernels of the layer call alone, through the C ABI exactly as the
+    # op launches them, on the same stream: KERNEL_BLOCKS blocks of K
+    # back-to-back launches of each, interleaved with blocks of K op layer
+    # calls, and the median block of each. The GPU sometimes runs a whole
+    # block of launches in a slower state (the same kernel 10-20 % slower for
+    # tens of launches, seen in rocprofv3 traces of identical launches), so
+    # a single block of one kind against a single block of another compares
+    # states, not kernels; interleaved medians compare the kernels.
     lib = capi.AttnLib()
     bq = 16 * plan.wm // G
     if 1 <= q_max < bq and planner.wm_for_rows(q_max * G) == plan.wm:
@@ -481,10 +464,17 @@ def measure_config(config: int, query_tokens: int, steps: int, warmup: int, cpu_
                                softmax_scale=scale, ws_o=ws_o, ws_lse=ws_lse, window=window)
                 for c, qq, ql in sets]
     sp = stream.cuda_stream
-    attn_ms, comb_ms = _kernel_events_ms(
-        stream, steps,
-        lambda i: lib.check(lib.attention_kernel(arg_sets[i % copies], sp)),
-        (lambda i: lib.check(lib.combine_kernel(arg_sets[i % copies], sp))) if S > 1 else None)
+    blocks = {"layer": [], "attention": [], "combine": []}
+    for _ in range(KERNEL_BLOCKS):
+        blocks["layer"].append(_events_ms(stream, steps, step))
+        blocks["attention"].append(_events_ms(
+            stream, steps, lambda i: lib.check(lib.attention_kernel(arg_sets[i % copies], sp))))
+        if S > 1:
+            blocks["combine"].append(_events_ms(
+                stream, steps, lambda i: lib.check(lib.combine_kernel(arg_sets[i % copies], sp))))
+    attn_ms = statistics.median(blocks["attention"])
+    comb_ms = statistics.median(blocks["combine"]) if S > 1 else None
+    layer_blocks_ms = statistics.median(blocks["layer"])
 
     # The same layer calls replayed from a captured graph (the reference times
     # graph-replayed launches): the median over GRAPH_REPLAYS replays of 20 calls each
@@ -523,6 +513,7 @@ def measure_config(config: int, query_tokens: int, steps: int, warmup: int, cpu_
         "plan": {"wm": plan.wm, "num_splits": S},
         "us_per_layer_call": round(ms * 1e3, 2),
         "us_per_layer_call_graph_median": None if graph_us is None else round(graph_us, 2),
+        "us_per_layer_call_block_median": round(layer_blocks_ms * 1e3, 2),
         "kernels_us": {"attention": round(attn_ms * 1e3, 2),
                        "combine": None if comb_ms is None else round(comb_ms * 1e3, 2)},
         "algorithmic_bytes": byts, "flops": flops,

@@ -133,16 +133,27 @@ __device__ __forceinline__ void make_block(const AttnParams& p, const RowTile& t
 // decode batch whose long decodes came last left some work-groups a decode
 // block behind the others).
 //
-// Each work-group walks its rounds starting at round t mod R (R rounds in
-// all; t = b mod (W / H), its row-tile slot, H KV heads) and wraps around:
-// the same blocks, in a rotated order, the H work-groups that take the H KV
-// heads of a row tile in the same round (adjacent heads' cells share cache
-// lines). In a mixed
-// batch the decode blocks (HBM-bound, ranked last) then run at different
-// times on different compute units, beside other units' prefill blocks
-// (MFMA-bound), instead of all at the end, where every unit streamed decode
-// keys at once and HBM bounded them (config 5: 4.84 ms, the sum of its
-// prefill part alone, 3.95 ms, and its decode part alone, 0.89 ms).
+// Placement. Work-groups are dealt to the 8 XCDs in turn (work-group b on
+// XCD b mod 8), and each XCD has its own L2. In a round of decode blocks,
+// slot H t + h (KV head h of the round's t-th row tile) goes to work-group
+// h M + t (M = W / H): the H heads of a row tile, whose 264-byte cells share
+// 128-byte lines, run on one XCD. In a round of wide (prefill) blocks, slot
+// s goes to work-group s: with H dividing 8, KV head h runs on the XCDs
+// x with x mod H = h, so the row tiles of one head, which read the same keys, share
+// an L2 (config 5: 4,562 -> 4,417 us; its prefill blocks had fetched 2.65 GB
+// for their 0.2 GB of keys with one row tile's heads per XCD). A round is
+// wide when its first unit lies among the wide requests' units, which rank
+// first.
+//
+// Each work-group walks its rounds starting at round x mod R (R rounds in
+// all, x its XCD) and wraps around: the same blocks, in a rotated order, all
+// work-groups of an XCD in the same round (so the row tiles of a head or the
+// heads of a row tile run at the same time). In a mixed batch the decode
+// blocks (HBM-bound, ranked last) then run at different times on different
+// XCDs, beside other XCDs' prefill blocks (MFMA-bound), instead of all at the
+// end, where every unit streamed decode keys at once and HBM bounded them
+// (config 5: 4.84 ms, the sum of its prefill part alone, 3.95 ms, and its
+// decode part alone, 0.89 ms).
 template <bool kWindow>
 struct BlockWalk {
   int r0 = -64;
@@ -153,6 +164,7 @@ struct BlockWalk {
   int total = -1;  // units of the launch (-1: not counted yet)
   int nrounds = 0;
   int rot = 0;     // the work-group's first round
+  int n_wide = 0;  // units of wide-block requests (ranked first), first group only
 
   // Moves to the next group of 64 requests: their ranks and the prefix sum
   // of their units. False past the last request.
@@ -189,9 +201,23 @@ struct BlockWalk {
   }
 
   // Units of the whole launch: the first group's prefix sum when it holds
-  // every request, else a count over all requests.
+  // every request (and n_wide: the units of its requests with more than 128
+  // rows, whose blocks are wide), else a count over all requests.
   __device__ __forceinline__ int count_units(const AttnParams& p, int lane) {
-    if (p.num_reqs <= 64) return scan_group(p, lane) ? u1 : 0;
+    if (p.num_reqs <= 64) {
+      if (!scan_group(p, lane)) return 0;
+      const int r = lane;
+      int wide = 0;
+      if (r < p.num_reqs) {
+        const int q_len = p.qsl[r + 1] - p.qsl[r];
+        if (q_len * p.group > 2 * kBlockRows / 4)
+          wide = request_row_tiles(q_len, p.blk_tok) * p.num_kv_heads;
+      }
+#pragma unroll
+      for (int dd = 32; dd >= 1; dd >>= 1) wide += __shfl_xor(wide, dd);
+      n_wide = __builtin_amdgcn_readfirstlane(wide);
+      return u1;
+    }
     int n = 0;
     for (int g = 0; g < p.num_reqs; g += 64) {
       const int r = g + lane;
@@ -208,22 +234,25 @@ struct BlockWalk {
     const int b = blockIdx.x;
     const int H = p.num_kv_heads;
     const int M = W % H == 0 ? W / H : 0;
-    // The work-group's slot in every round: slot H t + h (KV head h of the
-    // round's t-th row tile) is work-group h M + t (M = W / H). Work-groups
-    // are dealt to the 8 XCDs in turn, so with M a multiple of 8 (a full
-    // grid of 256) the H heads of a row tile run on one XCD.
+    // The work-group's slot in a decode round: slot H t + h (KV head h of the
+    // round's t-th row tile) is work-group h M + t (M = W / H); with M a
+    // multiple of 8 (a full grid of 256) the H heads of a row tile run on one
+    // XCD.
     const int slot = M > 0 ? (b % M) * H + b / M : b;
     if (total < 0) {
       total = count_units(p, lane);
       nrounds = (total + W - 1) / W;
-      rot = nrounds > 1 ? (slot / H) % nrounds : 0;
+      rot = nrounds > 1 ? (b % 8) % nrounds : 0;
     }
     int u;
     do {
       if (round >= nrounds) return false;
       const int rr = round + rot < nrounds ? round + rot : round + rot - nrounds;
       ++round;
-      u = rr * W + ((rr & 1) ? W - 1 - slot : slot);
+      // Rounds of wide blocks (prefill): slot b, so that the row tiles of one
+      // KV head, which read the same keys, share an XCD's L2.
+      const int sl = rr * W < n_wide ? b : slot;
+      u = rr * W + ((rr & 1) ? W - 1 - sl : sl);
     } while (u >= total);
     if (u < u0) {  // a wrapped round: scan again from the first group
       r0 = -64;
