@@ -547,9 +547,13 @@ __device__ __forceinline__ void compute_chunk_t(const Unit& U, const Lanes& L, i
       }
     }
   }
-  const float mx = xor_max(max8_raw(t));
-  const bool grow = mx > rescale_threshold(fresh);
-  if (__ballot(grow) != 0) {
+  // A row's max exceeds the threshold iff one of its 4 lanes' maxima does:
+  // the cross-lane reduction runs only when some row grows (rarely, past the
+  // first chunks).
+  const float lane_mx = max8_raw(t);
+  if (__ballot(lane_mx > rescale_threshold(fresh)) != 0) {
+    const float mx = xor_max(lane_mx);
+    const bool grow = mx > rescale_threshold(fresh);
     // Rows that keep m (also rows with no visible key yet) scale by 1.
     const float alpha = grow && !fresh ? __builtin_amdgcn_exp2f(-mx) : 1.0f;
     st.l *= alpha;

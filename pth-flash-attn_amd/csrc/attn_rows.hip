@@ -558,9 +558,12 @@ __device__ __forceinline__ void compute_rows(const RowSet& R, const Lanes (&L)[2
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     if (i >= ng) continue;
-    const float mx = xor_max(max8_raw(t[i]));
-    const bool grow = mx > rescale_threshold(fresh[i]);
-    if (__ballot(grow) != 0) {
+    // A row's max exceeds the threshold iff one of its 4 lanes' maxima does:
+    // the cross-lane reduction runs only when some row grows.
+    const float lane_mx = max8_raw(t[i]);
+    if (__ballot(lane_mx > rescale_threshold(fresh[i])) != 0) {
+      const float mx = xor_max(lane_mx);
+      const bool grow = mx > rescale_threshold(fresh[i]);
       const float alpha = grow && !fresh[i] ? __builtin_amdgcn_exp2f(-mx) : 1.0f;
       st[i].l *= alpha;
 #pragma unroll
@@ -702,10 +705,20 @@ __device__ __forceinline__ void convert_share(uint32_t slot, uint32_t copy, cons
                : "memory");
   const bf16x8 ka = i8x8_to_bf16(kw[0], kw[1]);
   // V column: the 8 keys in e order (tv(e) = 16 (e / 4) + 4 g + e % 4).
-  f16x8 va;
+  // Keys e, e + 1 into the low and high halves of one dword: int16 -> fp16,
+  // exact, the second through SDWA into the upper word (one instruction per
+  // value; the compiler's form converts and then packs).
+  u32x4 vp;
 #pragma unroll
-  for (int e = 0; e < 8; ++e)
-    va[e] = static_cast<_Float16>(static_cast<float>(static_cast<int32_t>(vb[e])));
+  for (int d = 0; d < 4; ++d) {
+    uint32_t w;
+    asm("v_cvt_f16_i16_e32 %0, %1\n\t"
+        "v_cvt_f16_i16_sdwa %0, %2 dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:WORD_0"
+        : "=&v"(w)
+        : "v"(vb[2 * d]), "v"(vb[2 * d + 1]));
+    vp[d] = w;
+  }
+  const f16x8 va = __builtin_bit_cast(f16x8, vp);
   const uint32_t dst = copy + wave * 1024 + lane * 16;
   ds_write16<0>(dst, __builtin_bit_cast(u32x4, ka));
   ds_write16<8192>(dst, __builtin_bit_cast(u32x4, va));
