@@ -565,11 +565,11 @@ __device__ __forceinline__ void compute_chunk_t(const Unit& U, const Lanes& L, i
     st.m = grow ? m_use + mx : st.m;
   }
   float pv[8];
-  float lsum = 0.0f;
+  float lsum;  // the sum starts at the first term (an added 0 is an instruction)
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     const float pe = __builtin_amdgcn_exp2f(t[e]);
-    lsum += pe;
+    lsum = e == 0 ? pe : lsum + pe;
     pv[e] = pe * vs[e];
   }
   st.l += lsum;

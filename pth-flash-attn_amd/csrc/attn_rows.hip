@@ -574,11 +574,11 @@ __device__ __forceinline__ void compute_rows(const RowSet& R, const Lanes (&L)[2
       st[i].m = grow ? m_use[i] + mx : st[i].m;
     }
     float pv[8];
-    float lsum = 0.0f;
+    float lsum;  // the sum starts at the first term (an added 0 is an instruction)
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const float pe = __builtin_amdgcn_exp2f(t[i][e]);
-      lsum += pe;
+      lsum = e == 0 ? pe : lsum + pe;
       pv[e] = pe * vs[e];
     }
     st[i].l += lsum;
@@ -614,9 +614,10 @@ constexpr int kCopyBase = kWideSlots * kSlotBytes;
 constexpr int kCopyExp = kCopyBase + kCopies * kCopyBytes;
 static_assert(kCopyExp + 4 * kCopies <= kRowSlots * kSlotBytes, "wide-block LDS");
 
+template <int kOff>
 __device__ __forceinline__ uint32_t ds_read_i8(uint32_t a) {
   uint32_t v;
-  asm volatile("ds_read_i8 %0, %1" : "=v"(v) : "v"(a));
+  asm volatile("ds_read_i8 %0, %1 offset:%2" : "=v"(v) : "v"(a), "n"(kOff));
   return v;
 }
 __device__ __forceinline__ void ds_write4(uint32_t a, float v) {
@@ -695,8 +696,8 @@ __device__ __forceinline__ void convert_share(uint32_t slot, uint32_t copy, cons
   uint32_t vb[8];
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
-    vb[q] = ds_read_i8(slot + o.v[q]);
-    vb[4 + q] = ds_read_i8(slot + o.v[q] + 2048);
+    vb[q] = ds_read_i8<0>(slot + o.v[q]);
+    vb[4 + q] = ds_read_i8<2048>(slot + o.v[q]);
   }
   asm volatile("s_waitcnt lgkmcnt(0)"
                : "+v"(kw), "+v"(vb[0]), "+v"(vb[1]), "+v"(vb[2]), "+v"(vb[3]), "+v"(vb[4]),
