@@ -507,6 +507,13 @@ struct ChunkOps {
   __device__ __forceinline__ bf16x8 v(int j) const { return column_to_bf16(ch.v, j); }
 };
 
+// The rest of a chunk step after QK: t = the lane's 8 scores minus m_use (log2
+// units), vs its V scales.
+template <int D, class Ops>
+__device__ __forceinline__ void chunk_tail(const Unit& U, const Lanes& L, int c, const Ops& ops,
+                                           float (&t)[8], float (&vs)[8], bool fresh, float m_use,
+                                           StateT<D>& st);
+
 template <int D, bool kF16Q, class Ops>
 __device__ __forceinline__ void compute_chunk_t(const Unit& U, const Lanes& L, int c,
                                                 const Ops& ops,
@@ -535,6 +542,13 @@ __device__ __forceinline__ void compute_chunk_t(const Unit& U, const Lanes& L, i
 #pragma unroll
     for (int i = 0; i < 4; ++i) t[4 * sub + i] = fmaf(acc[i], ks[4 * sub + i], -m_use);
   }
+  chunk_tail<D>(U, L, c, ops, t, vs, fresh, m_use, st);
+}
+
+template <int D, class Ops>
+__device__ __forceinline__ void chunk_tail(const Unit& U, const Lanes& L, int c, const Ops& ops,
+                                           float (&t)[8], float (&vs)[8], bool fresh, float m_use,
+                                           StateT<D>& st) {
   if (c < U.w_lo_max || c + kChunkTokens - 1 > U.w_hi_min) {
     // A key outside the row's range (or the request) gets p = 0 and a zero
     // V scale: its cache bytes may be any bits, a scale included.
@@ -603,6 +617,127 @@ __device__ __forceinline__ void compute_chunk(const Unit& U, const Lanes& L, int
                                               const bf16x8 (&qlo)[4], float scl,
                                               State& st) {
   compute_chunk_t<128, kF16Q>(U, L, c, ChunkOps{ch}, qb, qlo, scl, st);
+}
+
+// ---------------------------------------------------------------------------
+// Integer QK for the D = 128 paged kernels. The K bytes of a chunk are the A
+// operand of v_mfma_i32_16x16x64_i8 as they are loaded (lane (r, g) holds
+// bytes [32 g + 16 h, 32 g + 16 h + 16) of key r for product h = 0, 1), so K
+// is never converted. The query is scaled by 2^S and rounded to an integer x
+// with |x| < 2^20 (S from the unit's largest |q|, one exponent for the whole
+// wave), written as three signed digits x = d0 2^14 + d1 2^7 + d2 (d0 in
+// [-64, 63], d1, d2 in [0, 127]), and each digit is the B operand of one
+// integer product. The products are exact in int32; the score is
+// (2^14 acc0 + (2^7 acc1 + acc2)) 2^-S: the inner sum is exact in int32 and
+// one fp32 fma joins it to the exact 2^14 acc0, so a score carries one fp32
+// rounding. A query element is exact when it lies within 2^-13 (bf16) or
+// 2^-10 (fp16) of the largest |q| in binary order of magnitude; a smaller one
+// is rounded to 2^-20 of the largest, below the fp32 rounding of the score.
+// 2^-S is folded into the lanes' K-scale factor. A non-finite query element
+// makes every score of the unit NaN.
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+
+struct QInt8 {
+  i32x4 d[3][2];  // [digit][h]: digits of the lane's 16 query bytes of product h
+  float kadj;     // factor on the lane's scale factor: 2^-S (K-scale lanes) or 1
+};
+
+__device__ __forceinline__ float wave_max_abs(float x) {
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) x = fmaxf(x, __shfl_xor(x, d));
+  return x;
+}
+
+template <bool kF16Q>
+__device__ __forceinline__ void load_q_int8(const AttnParams& p, const Lanes& L, QInt8& q) {
+  u32x4 raw[4];
+  load_q_raw<128>(p, L, raw);
+  float f[32];  // raw[j] element e: query column 32 g + 8 j + e
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    if constexpr (kF16Q) {
+      const f16x8 h = __builtin_bit_cast(f16x8, raw[j]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) f[8 * j + e] = static_cast<float>(h[e]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const uint32_t w = raw[j][e >> 1];
+        f[8 * j + e] = __builtin_bit_cast(float, (e & 1) ? (w & 0xffff0000u) : (w << 16));
+      }
+    }
+  }
+  float amax = 0.0f;
+  bool bad = false;  // an element that is inf or NaN
+#pragma unroll
+  for (int e = 0; e < 32; ++e) {
+    amax = fmaxf(amax, fabsf(f[e]));
+    bad |= !(fabsf(f[e]) <= 3.402823466e38f);
+  }
+  amax = wave_max_abs(amax);
+  const bool finite = __ballot(bad) == 0;
+  // amax < 2^E with E the exponent field - 126 (E clamped so that 2^-S stays
+  // a normal float); S = 20 - E gives |q| 2^S < 2^20.
+  int E = static_cast<int>((__builtin_bit_cast(uint32_t, amax) >> 23) & 0xff) - 126;
+  E = E < -100 ? -100 : E;
+  const int S = __builtin_amdgcn_readfirstlane(20 - E);
+  q.kadj = L.r16 < 8 ? (finite ? __builtin_ldexpf(1.0f, -S) : __builtin_nanf("")) : 1.0f;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      uint32_t b0 = 0, b1 = 0, b2 = 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        // product h, byte 4 w + i: column 32 g + 16 h + 4 w + i = f[16 h + 4 w + i]
+        const float v = finite ? f[16 * h + 4 * w + i] : 0.0f;
+        const int x = static_cast<int>(__builtin_rintf(__builtin_ldexpf(v, S)));
+        b0 |= (static_cast<uint32_t>(x >> 14) & 0xffu) << (8 * i);
+        b1 |= (static_cast<uint32_t>(x >> 7) & 0x7fu) << (8 * i);
+        b2 |= (static_cast<uint32_t>(x) & 0x7fu) << (8 * i);
+      }
+      q.d[0][h][w] = static_cast<int32_t>(b0);
+      q.d[1][h][w] = static_cast<int32_t>(b1);
+      q.d[2][h][w] = static_cast<int32_t>(b2);
+    }
+  }
+}
+
+__device__ __forceinline__ i32x4 mfma_i8(const u32x4& a, const i32x4& b, i32x4 c) {
+  return __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i32x4, a), b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ void compute_chunk(const Unit& U, const Lanes& L, int c,
+                                              const Chunk& ch, const QInt8& q, float scl,
+                                              State& st) {
+  const ChunkOps ops{ch};
+  const float sc1 = ops.sc() * (scl * q.kadj);
+  const float ks[8] = {row_bcast<0>(sc1), row_bcast<1>(sc1), row_bcast<2>(sc1),
+                       row_bcast<3>(sc1), row_bcast<4>(sc1), row_bcast<5>(sc1),
+                       row_bcast<6>(sc1), row_bcast<7>(sc1)};
+  float vs[8] = {row_bcast<8>(sc1),  row_bcast<9>(sc1),  row_bcast<10>(sc1),
+                 row_bcast<11>(sc1), row_bcast<12>(sc1), row_bcast<13>(sc1),
+                 row_bcast<14>(sc1), row_bcast<15>(sc1)};
+  const bool fresh = st.m == kNegInf;
+  const float m_use = fresh ? 0.0f : st.m;
+  float t[8];
+#pragma unroll
+  for (int sub = 0; sub < 2; ++sub) {
+    i32x4 a0 = {0, 0, 0, 0}, a1 = {0, 0, 0, 0}, a2 = {0, 0, 0, 0};
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      a0 = mfma_i8(ch.k[sub][h], q.d[0][h], a0);
+      a1 = mfma_i8(ch.k[sub][h], q.d[1][h], a1);
+      a2 = mfma_i8(ch.k[sub][h], q.d[2][h], a2);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float sc = fmaf(static_cast<float>(a0[i]), 16384.0f,
+                            static_cast<float>(a1[i] * 128 + a2[i]));
+      t[4 * sub + i] = fmaf(sc, ks[4 * sub + i], -m_use);
+    }
+  }
+  chunk_tail<128>(U, L, c, ops, t, vs, fresh, m_use, st);
 }
 
 // A finished unit's result, held in registers until it is stored.

@@ -11,7 +11,9 @@
 //  * attn_fwd_pagerows (the vLLM NHD cell of 8 KV heads, work-groups whose
 //    8 waves are the 8 heads of the same keys): the work-group loads whole
 //    slot rows (every cache line by exactly one wave) into a shared LDS
-//    chunk buffer, one barrier per chunk;
+//    chunk buffer, one barrier per chunk; its QK products are integer (the
+//    int8 K bytes against three int8 digits of the scaled query, QInt8 in
+//    attn_device.h), so K is never converted;
 //  * attn_fwd_staged (any other cell cache): each wave loads its own head's
 //    cells in row order (lane (t, c) reads 16-byte piece c of key t, so one
 //    instruction covers 8 whole 128-byte rows) into its own LDS slot.
@@ -355,8 +357,8 @@ void attn_fwd_pagerows(const AttnParams p) {
     RowStaged S;
     ChunkPages cp = chunk_pages(p, U, U.c_begin);
     rows_load(p, cp, L, S);
-    bf16x8 qb[4], qlo[4];
-    load_q<kF16Q>(p, Ls, qb, qlo);
+    QInt8 qd;
+    load_q_int8<kF16Q>(p, Ls, qd);
     if (U.n_chunks > 1) cp = chunk_pages(p, U, U.c_begin + kChunkTokens);
     State st;
     state_reset(st);
@@ -372,7 +374,7 @@ void attn_fwd_pagerows(const AttnParams p) {
       __syncthreads();  // the chunk's rows are in the buffer
       Chunk ch;
       rows_read(buf, p, U.kvh, lane, ch);
-      compute_chunk<kF16Q>(U, Ls, U.c_begin + kChunkTokens * k, ch, qb, qlo, scl, st);
+      compute_chunk(U, Ls, U.c_begin + kChunkTokens * k, ch, qd, scl, st);
     }
     epilogue(p, U, Ls, st);
   }
