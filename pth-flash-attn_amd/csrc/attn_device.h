@@ -623,30 +623,26 @@ __device__ __forceinline__ void compute_chunk(const Unit& U, const Lanes& L, int
 // Integer QK for the D = 128 paged kernels. The K bytes of a chunk are the A
 // operand of v_mfma_i32_16x16x64_i8 as they are loaded (lane (r, g) holds
 // bytes [32 g + 16 h, 32 g + 16 h + 16) of key r for product h = 0, 1), so K
-// is never converted. The query is scaled by 2^S and rounded to an integer x
-// with |x| < 2^20 (S from the unit's largest |q|, one exponent for the whole
-// wave), written as three signed digits x = d0 2^14 + d1 2^7 + d2 (d0 in
-// [-64, 63], d1, d2 in [0, 127]), and each digit is the B operand of one
-// integer product. The products are exact in int32; the score is
-// (2^14 acc0 + (2^7 acc1 + acc2)) 2^-S: the inner sum is exact in int32 and
-// one fp32 fma joins it to the exact 2^14 acc0, so a score carries one fp32
-// rounding. A query element is exact when it lies within 2^-13 (bf16) or
-// 2^-10 (fp16) of the largest |q| in binary order of magnitude; a smaller one
-// is rounded to 2^-20 of the largest, below the fp32 rounding of the score.
-// 2^-S is folded into the lanes' K-scale factor. A non-finite query element
-// makes every score of the unit NaN.
+// is never converted; the B side maps its bytes to the same columns, so a
+// product sums over all 128 columns whatever order the hardware reduces in.
+// Each query row is scaled by 2^S (S from the row's largest |q|) and rounded
+// to integers x with |x| < 2^20, written as three digits
+// x = d0 2^14 + d1 2^7 + d2 (d0 = x >> 14 in [-64, 63], d1, d2 in [0, 127]),
+// and each digit is the B operand of one integer product. The products are
+// exact in int32; the score is (2^14 acc0 + (2^7 acc1 + acc2)) 2^-S, the
+// inner sum exact in int32 and one fp32 fma joining it to 2^14 acc0 (with
+// 2^-S applied by the lane, whose row is fixed). A query element within
+// 2^-13 (bf16) or 2^-10 (fp16) of its row's largest in binary order of
+// magnitude is exact; a smaller one is rounded to 2^-20 of the row's largest,
+// below the fp32 rounding of the score. A non-finite query element makes its
+// row's scores NaN.
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 
 struct QInt8 {
   i32x4 d[3][2];  // [digit][h]: digits of the lane's 16 query bytes of product h
-  float kadj;     // factor on the lane's scale factor: 2^-S (K-scale lanes) or 1
+  float r;        // 2^-S of the lane's row (NaN for a row with a non-finite element)
+  float r14;      // 2^14 r
 };
-
-__device__ __forceinline__ float wave_max_abs(float x) {
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) x = fmaxf(x, __shfl_xor(x, d));
-  return x;
-}
 
 template <bool kF16Q>
 __device__ __forceinline__ void load_q_int8(const AttnParams& p, const Lanes& L, QInt8& q) {
@@ -667,21 +663,21 @@ __device__ __forceinline__ void load_q_int8(const AttnParams& p, const Lanes& L,
       }
     }
   }
-  float amax = 0.0f;
-  bool bad = false;  // an element that is inf or NaN
+  float amax = 0.0f, bad = 0.0f;  // bad: 1 for an element that is inf or NaN
 #pragma unroll
   for (int e = 0; e < 32; ++e) {
     amax = fmaxf(amax, fabsf(f[e]));
-    bad |= !(fabsf(f[e]) <= 3.402823466e38f);
+    bad = fabsf(f[e]) <= 3.402823466e38f ? bad : 1.0f;
   }
-  amax = wave_max_abs(amax);
-  const bool finite = __ballot(bad) == 0;
-  // amax < 2^E with E the exponent field - 126 (E clamped so that 2^-S stays
-  // a normal float); S = 20 - E gives |q| 2^S < 2^20.
+  amax = xor_max(amax);  // over the 4 lanes of the row
+  bad = xor_max(bad);
+  // amax < 2^E with E the exponent field - 126 (clamped so that 2^-S stays a
+  // normal float); S = 20 - E gives |q| 2^S < 2^20.
   int E = static_cast<int>((__builtin_bit_cast(uint32_t, amax) >> 23) & 0xff) - 126;
-  E = E < -100 ? -100 : E;
-  const int S = __builtin_amdgcn_readfirstlane(20 - E);
-  q.kadj = L.r16 < 8 ? (finite ? __builtin_ldexpf(1.0f, -S) : __builtin_nanf("")) : 1.0f;
+  E = E < -100 ? -100 : (E > 128 ? 128 : E);
+  const int S = 20 - E;
+  q.r = bad == 0.0f ? __builtin_ldexpf(1.0f, -S) : __builtin_nanf("");
+  q.r14 = 16384.0f * q.r;
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
 #pragma unroll
@@ -690,7 +686,7 @@ __device__ __forceinline__ void load_q_int8(const AttnParams& p, const Lanes& L,
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         // product h, byte 4 w + i: column 32 g + 16 h + 4 w + i = f[16 h + 4 w + i]
-        const float v = finite ? f[16 * h + 4 * w + i] : 0.0f;
+        const float v = bad == 0.0f ? f[16 * h + 4 * w + i] : 0.0f;
         const int x = static_cast<int>(__builtin_rintf(__builtin_ldexpf(v, S)));
         b0 |= (static_cast<uint32_t>(x >> 14) & 0xffu) << (8 * i);
         b1 |= (static_cast<uint32_t>(x >> 7) & 0x7fu) << (8 * i);
@@ -711,7 +707,7 @@ __device__ __forceinline__ void compute_chunk(const Unit& U, const Lanes& L, int
                                               const Chunk& ch, const QInt8& q, float scl,
                                               State& st) {
   const ChunkOps ops{ch};
-  const float sc1 = ops.sc() * (scl * q.kadj);
+  const float sc1 = ops.sc() * scl;
   const float ks[8] = {row_bcast<0>(sc1), row_bcast<1>(sc1), row_bcast<2>(sc1),
                        row_bcast<3>(sc1), row_bcast<4>(sc1), row_bcast<5>(sc1),
                        row_bcast<6>(sc1), row_bcast<7>(sc1)};
@@ -732,8 +728,8 @@ __device__ __forceinline__ void compute_chunk(const Unit& U, const Lanes& L, int
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const float sc = fmaf(static_cast<float>(a0[i]), 16384.0f,
-                            static_cast<float>(a1[i] * 128 + a2[i]));
+      const float sc = fmaf(static_cast<float>(a0[i]), q.r14,
+                            static_cast<float>(a1[i] * 128 + a2[i]) * q.r);
       t[4 * sub + i] = fmaf(sc, ks[4 * sub + i], -m_use);
     }
   }

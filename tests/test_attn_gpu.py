@@ -19,7 +19,7 @@ import pytest
 import torch
 
 from cases import (
-    Case, Batch, abs_v_batch, assert_parity, compare, launch_args, materialize, oracle_of,
+    LSE_ABS, Case, Batch, abs_v_batch, assert_parity, compare, launch_args, materialize, oracle_of,
     tile_tokens, uniform_lengths,
 )
 
@@ -424,6 +424,47 @@ def test_public_entry_points_windowed_verify(S, causal):
     res = compare(out, None, ref_out, ref_lse, valid)
     print(f"  S={S} causal={causal} -> {res}", flush=True)
     assert_parity(res, name=f"public window S={S}", strict=False)
+
+
+# ------------------------------------------------- page-row integer QK
+@pytest.mark.parametrize("q_dtype", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
+@pytest.mark.parametrize("S", [1, None], ids=["S1", "plan"])
+def test_pagerows_query_dynamic_range(q_dtype, S):
+    """The page-row kernel's integer QK scales each query row by its own power
+    of two and splits it into three int8 digits: rows whose magnitudes span
+    2^-12 .. 2^12 within one unit, and elements 2^-18 below their row's
+    largest (rounded to 2^-20 of it), must match the fp64 oracle beyond the
+    output's own rounding and meet the decode kernels' 1e-4 fp32-output
+    check."""
+    c = Case("pagerows-qrange", q_lens=[1, 1, 4, 1], seq_lens=[700, 2049, 4100, 33],
+             q_dtype=q_dtype, seed=31, num_splits=S)
+    print(f"case {c.name} {q_dtype} S={S}", flush=True)
+    b = materialize(c, DEV)
+    gen = torch.Generator(device="cpu").manual_seed(77)
+    T, Hq, D = b.q.shape
+    row = torch.pow(2.0, torch.randint(-12, 13, (T, Hq, 1), generator=gen).float())
+    small = torch.where(torch.rand(T, Hq, D, generator=gen) < 0.2,
+                        torch.tensor(2.0 ** -18), torch.tensor(1.0))
+    if q_dtype == torch.float16:
+        row = row.clamp(max=2.0 ** 8)  # |q| within fp16's range
+    b.q.copy_((b.q.float().cpu() * row * small).to(q_dtype).to(DEV))
+    out, lse = run_capi(b)
+    ref_out, ref_lse, valid = oracle_of(b, threads=16)
+    res = compare(out, None, ref_out, ref_lse, valid)
+    print(f"  -> {res}", flush=True)
+    # Rows scaled by 2^12 have scores of order 10^4 and near one-hot softmax:
+    # outputs of order |v| (bf16 storage alone rounds them by up to 8e-3), so
+    # the gate is on the error beyond that rounding; the log-sum-exp, of
+    # order 10^4, is checked relative to its size (fp32 keeps 24 bits).
+    assert_parity(res, name=c.name, strict=False)
+    le = np.abs(lse.float().cpu().numpy()[valid] - ref_lse[valid])
+    lim = LSE_ABS + 2.0 ** -20 * np.abs(ref_lse[valid])
+    print(f"  lse max abs {le.max():.3g}, worst error / limit {(le / lim).max():.3g}", flush=True)
+    assert (le <= lim).all()
+    out32, _ = run_capi(b, out_dtype=torch.float32)
+    r32 = compare(out32, None, ref_out, ref_lse, valid)
+    print(f"  fp32 out -> max abs {r32['max_abs']:.3g} (gate {F32_MAX_ABS:g})", flush=True)
+    assert r32["max_abs"] <= F32_MAX_ABS
 
 
 # ---------------------------------------------------------------- configs 2-5
