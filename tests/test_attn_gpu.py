@@ -467,6 +467,32 @@ def test_pagerows_query_dynamic_range(q_dtype, S):
     assert r32["max_abs"] <= F32_MAX_ABS
 
 
+def test_pagerows_nonfinite_query_row():
+    """A non-finite query element (NaN or inf) makes its own row's output
+    non-finite, as a float QK product would, and leaves the other rows of the
+    same unit exact (the integer QK scales each row on its own)."""
+    c = Case("pagerows-nonfinite-q", q_lens=[1, 4], seq_lens=[900, 3000], seed=41)
+    b = materialize(c, DEV)
+    bad = [(0, 5, 17, float("nan")), (2, 9, 100, float("inf"))]  # (token, head, column, value)
+    for tok, head, col, val in bad:
+        b.q[tok, head, col] = val
+    out, _ = run_capi(b, num_splits=1)
+    o = out.float().cpu().numpy()
+    for tok, head, _, _ in bad:
+        assert not np.isfinite(o[tok, head]).any(), (tok, head)
+    hb = Batch(c, b.cache.to("cpu"), b.q.cpu(), b.qsl.cpu())
+    q_ok = hb.q.clone()
+    for tok, head, col, _ in bad:
+        q_ok[tok, head, col] = 0.0
+    ref_out, ref_lse, valid = oracle_of(Batch(c, hb.cache, q_ok, hb.qsl), threads=16)
+    keep = np.repeat(valid[:, None], c.Hq, axis=1)  # (token, head) rows to compare
+    for tok, head, _, _ in bad:
+        keep[tok, head] = False
+    err = np.abs(o[keep].astype(np.float64) - ref_out[keep])
+    print(f"  other rows -> max abs {err.max():.3g}, mean abs {err.mean():.3g}", flush=True)
+    assert err.max() <= 2e-3 and err.mean() <= 2e-4
+
+
 # ---------------------------------------------------------------- configs 2-5
 def test_config2_batched_decode():
     """Config 2: 64 seqs, q=1, 32q/8kv, L ~ U[1k, 32k], BS 16."""
