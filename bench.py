@@ -560,8 +560,8 @@ def xcd_spread(steps: int, warmup: int, cus: int, config: int = 2, query_tokens:
     """Start and finishing times of the page-row attention kernel by XCD on a
     configuration it runs (2 or 3): the kernel as bench_hip/build.py builds it
     with PA_WAVE_CLOCK (each wave records its XCD and its start and end time,
-    s_memrealtime at 100 MHz), launched alone through the C ABI like the
-    kernel-alone loop of measure_config; per launch, every time relative to
+    s_memrealtime at 100 MHz), launched through the C ABI after three
+    back-to-back layer calls (attention, then combine); per launch, every time relative to
     the launch's first wave start; reported as medians over `steps`
     launches. Records left by waves of earlier launches (slots beyond this
     grid) are those that started more than 30 µs before the last start."""
@@ -606,10 +606,18 @@ def xcd_spread(steps: int, warmup: int, cus: int, config: int = 2, query_tokens:
     for _ in range(max(warmup, 10)):
         lib.check(lib.attention_kernel(args, sp))
     torch.cuda.synchronize()
-    per_xcd_mean, per_xcd_p10, per_xcd_p90, last = {}, {}, {}, []
+    per_xcd_mean, per_xcd_p10, per_xcd_p90, per_xcd_start, last = {}, {}, {}, {}, []
     overall = {k: [] for k in ("start_p50", "start_p90", "start_max", "end_p10", "end_p50", "end_p90")}
     counted = []
     for _ in range(steps):
+        # Three layer calls back to back before the recorded launch: its
+        # work-groups then start as the previous call's combine drains, as
+        # in the timed loops (after an idle gap, the XCDs' first work-groups
+        # start up to 4 us apart; back to back, within 0.4 us).
+        for _r in range(3):
+            lib.check(lib.attention_kernel(args, sp))
+            if S > 1:
+                lib.check(lib.combine_kernel(args, sp))
         lib.check(lib.attention_kernel(args, sp))
         torch.cuda.synchronize()
         if read(buf.ctypes.data, waves) != 0:
@@ -629,6 +637,7 @@ def xcd_spread(steps: int, warmup: int, cus: int, config: int = 2, query_tokens:
         for k in np.unique(xcd):
             e = end[xcd == k]
             per_xcd_mean.setdefault(int(k), []).append(float(e.mean()))
+            per_xcd_start.setdefault(int(k), []).append(float(np.median(start[xcd == k])))
             per_xcd_p10.setdefault(int(k), []).append(float(np.percentile(e, 10)))
             per_xcd_p90.setdefault(int(k), []).append(float(np.percentile(e, 90)))
     med = statistics.median
@@ -637,7 +646,8 @@ def xcd_spread(steps: int, warmup: int, cus: int, config: int = 2, query_tokens:
         "waves": int(med(counted)), "num_splits": S,
         "last_wave_end_us": round(med(last), 1),
         "all_waves_us": {k: round(med(v), 1) for k, v in overall.items()},
-        "by_xcd": {k: {"mean_end_us": round(med(v), 1),
+        "by_xcd": {k: {"start_p50_us": round(med(per_xcd_start[k]), 2),
+                       "mean_end_us": round(med(v), 1),
                        "p10_end_us": round(med(per_xcd_p10[k]), 1),
                        "p90_end_us": round(med(per_xcd_p90[k]), 1)}
                    for k, v in sorted(per_xcd_mean.items())},
