@@ -347,7 +347,7 @@ void attn_fwd_pagerows(const AttnParams p) {
   const int L = threadIdx.x;
   const float scl = scale_factor(lane & 15, p.scale_log2);
   Work<kWindow, kStream> work;
-  work.init(p, lane);
+  work.template init<false>(p, lane);
   Unit U;
   Lanes Ls;
   int it = 0;  // chunks processed by the work-group (buffer parity)

@@ -124,6 +124,25 @@ struct StreamCursor {
   int64_t incl = 0;
 };
 
+// stream_per that also loads the cursor's first window when the launch has
+// at most 64 requests: the loads that size the partition then also serve the
+// first stream_locate, which otherwise reads the requests' lengths again
+// before it can find the wave's first stream (one memory round trip fewer
+// on the way to the first chunk).
+__device__ __forceinline__ int64_t stream_per_cursor(const StreamDesc& d, int lane,
+                                                     int64_t& total, StreamCursor& c) {
+  if (d.num_reqs > 64) return stream_per(d, lane, total);
+  int64_t pos = 0;
+  int32_t mx = 0;
+  if (lane < d.num_reqs) request_positions(d, lane, pos, mx);
+  c.r0 = 0;
+  c.base = 0;
+  c.incl = wave_scan64(pos, lane);
+  c.end = readlane64(c.incl, 63);
+  total = c.end;
+  return chunks_per_group(total, wave_max32(mx), d.num_wg, d.num_splits);
+}
+
 // The stream holding position P (P never decreases on a cursor). False when
 // P is past the last stream.
 __device__ __forceinline__ bool stream_locate(const StreamDesc& d, StreamCursor& c, int64_t P,
