@@ -65,9 +65,13 @@ __device__ __forceinline__ int32_t wave_max32(int32_t x) {
 // count of its longest row tile.
 __device__ __forceinline__ void request_positions(const StreamDesc& d, int r, int64_t& pos,
                                                   int32_t& longest) {
-  const int q_len = d.qsl[r + 1] - d.qsl[r];
+  int q0 = d.qsl[r], q1 = d.qsl[r + 1], sl = d.seq_lens[r];
+  // All three loads in flight together: left to itself the compiler sinks
+  // the seq_lens load into request_chunks' tile loop, behind the wait for
+  // the qsl loads, which made the partition two dependent round trips.
+  asm volatile("" : "+v"(q0), "+v"(q1), "+v"(sl));
   int32_t sum, mx;
-  request_chunks(q_len, d.seq_lens[r], d.bq, d.window, d.causal != 0, sum, mx);
+  request_chunks(q1 - q0, sl, d.bq, d.window, d.causal != 0, sum, mx);
   pos = static_cast<int64_t>(sum) * d.n_hg;
   longest = mx;
 }
@@ -160,11 +164,14 @@ __device__ __forceinline__ bool stream_locate(const StreamDesc& d, StreamCursor&
   }
   const int64_t local = P - c.base;
   const int j = static_cast<int>(__popcll(__ballot(c.incl <= local)));
-  const int r = c.r0 + j;
+  // r is wave-uniform; saying so makes the three reads scalar loads, and the
+  // empty asm keeps them in flight together (otherwise the seq_lens read is
+  // sunk into the tile loop below, behind the wait for the qsl reads).
+  const int r = __builtin_amdgcn_readfirstlane(c.r0 + j);
   int64_t at = c.base + (j > 0 ? readlane64(c.incl, j - 1) : 0);
-  const int q_start = ld_ro(d.qsl, r);
-  const int q_len = ld_ro(d.qsl, r + 1) - q_start;
-  const int seq_len = ld_ro(d.seq_lens, r);
+  int q_start = ld_ro(d.qsl, r), q_end = ld_ro(d.qsl, r + 1), seq_len = ld_ro(d.seq_lens, r);
+  asm volatile("" : "+s"(q_start), "+s"(q_end), "+s"(seq_len));
+  const int q_len = q_end - q_start;
   const int tiles = request_row_tiles(q_len, d.bq);
   for (int k = 0; k < tiles; ++k) {
     const RowTile t = request_tile(r, q_start, q_len, seq_len, d.bq, k);
