@@ -88,13 +88,13 @@ __device__ __forceinline__ int row_live_splits(const CombineParams& c, int r, in
   const int hu = (head / c.group) * c.n_rg + row / kRowsPerWave;
   int64_t at = positions_before(d, r, lane);
   for (int k = 0; k < j; ++k)
-    at += static_cast<int64_t>(tile_chunks(request_tile(r, q_start, q_len, seq_len, c.bq, k),
-                                           c.window, c.causal != 0)) *
+    at += static_cast<int64_t>(stream_span(tile_chunks(
+              request_tile(r, q_start, q_len, seq_len, c.bq, k), c.window, c.causal != 0))) *
           c.n_hg;
   const int32_t n = tile_chunks(request_tile(r, q_start, q_len, seq_len, c.bq, j), c.window,
                                 c.causal != 0);
   int first, live;
-  stream_splits(at + static_cast<int64_t>(hu / c.gu) * n, n, per, first, live);
+  stream_splits(at + static_cast<int64_t>(hu / c.gu) * stream_span(n), n, per, first, live);
   return live;
 }
 

@@ -321,10 +321,15 @@ struct Work {
           pos = stop;
           return false;
         }
-        const int c0 = static_cast<int>(pos - sp.c0);
-        const int64_t end = sp.c0 + sp.n < stop ? sp.c0 + sp.n : stop;
-        const int c1 = static_cast<int>(end - sp.c0);
+        // The work-group's chunks of this stream: [c0, c1). A range that
+        // holds only the stream's start positions has none (the next
+        // work-group starts the stream).
+        const int64_t cs = sp.c0 + kStreamStartPositions;
+        const int c0 = pos > cs ? static_cast<int>(pos - cs) : 0;
+        const int64_t end = cs + sp.n < stop ? cs + sp.n : stop;
+        const int c1 = static_cast<int>(end - cs);
         pos = end;
+        if (c1 <= c0) continue;
         const int hu = sp.hg * p.gu + wave;
         if (hu >= p.n_hu) continue;  // the group has fewer units than waves
         int first, live;

@@ -201,11 +201,25 @@ PA_HD int32_t request_row_tiles(int32_t q_len, int32_t bq) {
 // Split partition (num_splits > 1). The keys of every row tile, from a
 // 32-aligned base, are a stream of 32-key chunks; the streams of all
 // (request, row tile, group of 8 KV-head units) are laid end to end, in that
-// order, and work-group b of the grid takes positions [b per, (b + 1) per).
-// A stream cut by such a boundary is computed in parts (its splits), one per
-// work-group it meets, and merged by the LSE combine. Every work-group thus
-// gets the same number of chunks, and a stream only has as many splits as
-// the work-groups its length needs.
+// order, each preceded by kStreamStartPositions positions that hold no chunk,
+// and work-group b of the grid takes positions [b per, (b + 1) per). A stream
+// cut by such a boundary is computed in parts (its splits), one per
+// work-group whose range meets its chunks, and merged by the LSE combine.
+// The start positions price what a wave pays to begin a unit (its
+// block-table entry, query and first chunk arrive before its first chunk
+// step): a work-group whose range runs into a new stream gets that many
+// fewer chunks, so every work-group costs about per + one start, instead
+// of those crossing a stream boundary costing a start more than the rest.
+// A stream only has as many splits as the work-groups its chunks need.
+
+// Positions in front of each stream's chunks. Per-wave timestamps put a
+// unit's first chunk two to three chunk steps after the unit is known;
+// measured over 1 to 4 (A/B in one process): config 4 -2.5 us with any of
+// them, config 2 -1.5 / -2.8 / -3.3 / -1.4 us, so 3.
+constexpr int32_t kStreamStartPositions = 3;
+
+// Positions of a stream of n chunks.
+PA_HD int32_t stream_span(int32_t n) { return n > 0 ? n + kStreamStartPositions : 0; }
 
 // First key of chunk 0 of a row tile, and the number of chunks that cover the
 // keys any of its rows sees.
@@ -219,23 +233,24 @@ PA_HD int32_t tile_chunks(const RowTile& t, int32_t window, bool causal) {
   return re > base ? (re - base + kChunkTokens - 1) / kChunkTokens : 0;
 }
 
-// Sum and maximum of tile_chunks over the row tiles of a request.
-PA_HD void request_chunks(int32_t q_len, int32_t seq_len, int32_t bq, int32_t window,
-                          bool causal, int32_t& sum, int32_t& max) {
+// Positions (the sum of stream_span) and the largest tile_chunks over the
+// row tiles of a request.
+PA_HD void request_spans(int32_t q_len, int32_t seq_len, int32_t bq, int32_t window,
+                         bool causal, int32_t& sum, int32_t& max) {
   sum = 0;
   max = 0;
   const int32_t tiles = request_row_tiles(q_len, bq);
   for (int32_t j = 0; j < tiles; ++j) {
     const int32_t n = tile_chunks(request_tile(0, 0, q_len, seq_len, bq, j), window, causal);
-    sum += n;
+    sum += stream_span(n);
     max = n > max ? n : max;
   }
 }
 
-// Stream positions per work-group: an even share of `total`, but at least
-// kMinChunksPerSplit and enough that no stream of up to `max_n` chunks
-// meets more than num_splits work-groups (a stream of n chunks meets at most
-// ceil((n - 1) / per) + 1 of them). One chunk is the floor: a small launch
+// Stream positions per work-group: an even share of the `total` positions,
+// but at least kMinChunksPerSplit and enough that no stream of up to `max_n`
+// chunks meets more than num_splits work-groups (n consecutive chunk
+// positions meet at most ceil((n - 1) / per) + 1 of them). One chunk is the floor: a small launch
 // is a chain of dependent chunk loads per wave, so the shortest chain wins
 // (measured: config 1's layer call 20.3 us with a floor of 4 chunks, 16.5 us
 // with 1; long launches have shares far above the floor).
@@ -250,11 +265,14 @@ PA_HD int64_t chunks_per_group(int64_t total, int32_t max_n, int32_t num_wg, int
   return per;
 }
 
-// The work-groups a stream [c0, c0 + n) meets: first and count (its splits);
-// split s of the stream is work-group first + s.
+// The work-groups whose ranges meet the chunks of the stream of n chunks
+// that starts at position c0 (its chunks at [c0 + kStreamStartPositions,
+// + n)): first and count (its splits); split s of the stream is work-group
+// first + s.
 PA_HD void stream_splits(int64_t c0, int32_t n, int64_t per, int32_t& first, int32_t& live) {
-  first = static_cast<int32_t>(c0 / per);
-  live = n > 0 ? static_cast<int32_t>((c0 + n - 1) / per) - first + 1 : 1;
+  const int64_t cs = c0 + kStreamStartPositions;
+  first = static_cast<int32_t>(cs / per);
+  live = n > 0 ? static_cast<int32_t>((cs + n - 1) / per) - first + 1 : 1;
 }
 
 }  // namespace pa

@@ -67,11 +67,11 @@ __device__ __forceinline__ void request_positions(const StreamDesc& d, int r, in
                                                   int32_t& longest) {
   int q0 = d.qsl[r], q1 = d.qsl[r + 1], sl = d.seq_lens[r];
   // All three loads in flight together: left to itself the compiler sinks
-  // the seq_lens load into request_chunks' tile loop, behind the wait for
+  // the seq_lens load into request_spans' tile loop, behind the wait for
   // the qsl loads, which made the partition two dependent round trips.
   asm volatile("" : "+v"(q0), "+v"(q1), "+v"(sl));
   int32_t sum, mx;
-  request_chunks(q1 - q0, sl, d.bq, d.window, d.causal != 0, sum, mx);
+  request_spans(q1 - q0, sl, d.bq, d.window, d.causal != 0, sum, mx);
   pos = static_cast<int64_t>(sum) * d.n_hg;
   longest = mx;
 }
@@ -109,8 +109,9 @@ __device__ __forceinline__ int64_t positions_before(const StreamDesc& d, int r, 
   return readlane64(wave_scan64(sum, lane), 63);
 }
 
-// One stream: row tile t, group hg, positions [c0, c0 + n); chunk c of it
-// covers keys [cb + 32 c, cb + 32 c + 32).
+// One stream: row tile t, group hg, n chunks, positions [c0, c0 +
+// stream_span(n)) (chunk c at position c0 + kStreamStartPositions + c); chunk
+// c covers keys [cb + 32 c, cb + 32 c + 32).
 struct StreamPos {
   RowTile t;
   int32_t hg;
@@ -176,12 +177,13 @@ __device__ __forceinline__ bool stream_locate(const StreamDesc& d, StreamCursor&
   for (int k = 0; k < tiles; ++k) {
     const RowTile t = request_tile(r, q_start, q_len, seq_len, d.bq, k);
     const int32_t n = tile_chunks(t, d.window, d.causal != 0);
-    const int64_t span = static_cast<int64_t>(n) * d.n_hg;
+    const int32_t sn = stream_span(n);
+    const int64_t span = static_cast<int64_t>(sn) * d.n_hg;
     if (P < at + span) {
       out.t = t;
-      out.hg = static_cast<int32_t>((P - at) / n);
+      out.hg = static_cast<int32_t>((P - at) / sn);
       out.n = n;
-      out.c0 = at + static_cast<int64_t>(out.hg) * n;
+      out.c0 = at + static_cast<int64_t>(out.hg) * sn;
       out.cb = tile_chunk_base(t, d.window);
       return true;
     }

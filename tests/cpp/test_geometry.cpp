@@ -133,7 +133,7 @@ static void streams() {
         for (int causal = 0; causal < 2; ++causal)
           for (int bq : {1, 4, 16}) {
             int32_t sum = 0, mx = 0;
-            request_chunks(q, L, bq, W, causal, sum, mx);
+            request_spans(q, L, bq, W, causal, sum, mx);
             int32_t s2 = 0, m2 = 0;
             for (int j = 0; j < request_row_tiles(q, bq); ++j) {
               const RowTile t = request_tile(0, 0, q, L, bq, j);
@@ -148,10 +148,10 @@ static void streams() {
                 last_used |= hi >= cb + kChunkTokens * (n - 1);
               }
               CHECK(first_used && last_used, "no chunk wholly outside the keys");
-              s2 += n;
+              s2 += n + kStreamStartPositions;
               m2 = n > m2 ? n : m2;
             }
-            CHECK(sum == s2 && mx == m2, "request_chunks");
+            CHECK(sum == s2 && mx == m2, "request_spans");
           }
   std::mt19937 rng(3);
   for (int trial = 0; trial < 4000; ++trial) {
@@ -161,30 +161,40 @@ static void streams() {
     int32_t mx = 0;
     for (int& n : len) {
       n = 1 + rng() % (trial % 3 == 0 ? 5000 : 200);
-      total += n;
+      total += stream_span(n);
       mx = n > mx ? n : mx;
     }
     const int num_wg = 1 + rng() % 300;
     const int S = 2 + rng() % 300;
     const int64_t per = chunks_per_group(total, mx, num_wg, S);
     CHECK(per >= kMinChunksPerSplit && per * num_wg >= total, "per covers the total");
+    // Per work-group: its chunks plus kStreamStartPositions per unit (a
+    // stream whose chunks its range meets) never exceed per plus one start.
+    std::vector<int64_t> cost(num_wg, 0);
     int64_t c0 = 0;
     for (int n : len) {
       int first, live;
       stream_splits(c0, n, per, first, live);
       CHECK(live >= 1 && live <= S, "live %d > S %d (n=%d per=%lld)", live, S, n, (long long)per);
-      // Brute force: the work-groups whose range meets [c0, c0 + n).
+      // Brute force: the work-groups whose range meets the chunk positions
+      // [c0 + start, c0 + start + n).
+      const int64_t cs = c0 + kStreamStartPositions;
       int bf_first = -1, bf_count = 0;
       for (int b = 0; b < num_wg; ++b) {
         const int64_t lo = b * per, hi = lo + per;
-        if (lo < c0 + n && hi > c0) {
+        if (lo < cs + n && hi > cs) {
           if (bf_first < 0) bf_first = b;
           ++bf_count;
+          const int64_t a = lo > cs ? lo : cs, e = hi < cs + n ? hi : cs + n;
+          cost[b] += (e - a) + kStreamStartPositions;
         }
       }
       CHECK(bf_first == first && bf_count == live, "stream_splits");
-      c0 += n;
+      c0 += stream_span(n);
     }
+    for (int b = 0; b < num_wg; ++b)
+      CHECK(cost[b] <= per + kStreamStartPositions, "work-group %d cost %lld > per %lld + start", b,
+            (long long)cost[b], (long long)per);
   }
   std::printf("streams ok\n");
 }
