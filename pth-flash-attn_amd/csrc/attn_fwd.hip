@@ -116,19 +116,9 @@ __device__ __forceinline__ void reg_load(const AttnParams& p, const RegLoader& R
   ch.sc = *reinterpret_cast<const float*>(sb + R.off_s);
 }
 
-#ifdef EXP_REGCLK
-}  // namespace
-__device__ uint64_t reg_clock[8192 * 4];
-namespace {
-#endif
 template <bool kWindow, bool kStream, bool kF16Q>
 __global__ __launch_bounds__(kFwdWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void attn_fwd_paged_reg(const AttnParams p) {
-#ifdef EXP_REGCLK
-  const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
-  uint64_t t_unit = 0, t_c0 = 0, t_c1 = 0;
-  int n_units = 0, n_ch = 0;
-#endif
   const int lane = threadIdx.x & 63;
   const float scl = scale_factor(lane & 15, p.scale_log2);
   Work<kWindow, kStream> work;
@@ -136,11 +126,6 @@ void attn_fwd_paged_reg(const AttnParams p) {
   Unit U;
   while (work.next(p, lane, U)) {
     if (!U.has_rows) continue;
-#ifdef EXP_REGCLK
-    if (t_unit == 0) t_unit = __builtin_amdgcn_s_memrealtime();
-    ++n_units;
-    n_ch += U.n_chunks;
-#endif
     const Lanes L = unit_lanes<kWindow>(p, U, lane);
     State st;
     state_reset(st);
@@ -160,19 +145,7 @@ void attn_fwd_paged_reg(const AttnParams p) {
           reg_load(p, R, lane, cb);
           if (k + 2 < U.n_chunks) reg_pages(p, U, c + 2 * kChunkTokens, R);
         }
-#ifdef EXP_REGCLK
-        if (t_c0 == 0) {
-          asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-          t_c0 = __builtin_amdgcn_s_memrealtime();
-        }
-#endif
         compute_chunk<kF16Q>(U, L, c, ca, qb, qlo, scl, st);
-#ifdef EXP_REGCLK
-        if (t_c1 == 0) {
-          asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
-          t_c1 = __builtin_amdgcn_s_memrealtime();
-        }
-#endif
         if (++k >= U.n_chunks) break;
         if (k + 1 < U.n_chunks) {
           reg_load(p, R, lane, ca);
@@ -184,16 +157,6 @@ void attn_fwd_paged_reg(const AttnParams p) {
     }
     epilogue(p, U, L, st);
   }
-#ifdef EXP_REGCLK
-  const int w = static_cast<int>(blockIdx.x) * kFwdWaves + (static_cast<int>(threadIdx.x) >> 6);
-  if (lane == 0 && w < 8192) {
-    reg_clock[4 * w] = static_cast<uint64_t>(n_units) | (static_cast<uint64_t>(n_ch) << 16) |
-                       ((t_unit ? t_unit - t0 : 0) << 32);
-    reg_clock[4 * w + 1] = t0;
-    reg_clock[4 * w + 2] = (t_c0 ? t_c0 - t0 : 0) | ((t_c1 ? t_c1 - t0 : 0) << 32);
-    reg_clock[4 * w + 3] = __builtin_amdgcn_s_memrealtime() - t0;
-  }
-#endif
 }
 
 // Windows up to this many keys: the register-load kernel (its short
@@ -227,9 +190,4 @@ hipError_t launch_fwd_kernel(const AttnParams& p, dim3 grid, bool windowed,
                       : launch_variant<false, false>(p, grid, q_f16, stream);
 }
 
-#ifdef EXP_REGCLK
-extern "C" int32_t pth_attn_debug_reg_clock(uint64_t* dst, int64_t waves) {
-  return hipMemcpyFromSymbol(dst, HIP_SYMBOL(pa::reg_clock), waves * 4 * sizeof(uint64_t)) == hipSuccess ? 0 : 1;
-}
-#endif
 }  // namespace pa
