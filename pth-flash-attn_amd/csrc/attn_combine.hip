@@ -11,9 +11,11 @@
 // or uninitialised memory) never enters an arithmetic operation; the sums run
 // in the fixed order s = 0..S-1, so the result is deterministic.
 //
-// Few rows with many splits (shared_rows): a work-group of 16 waves takes one
-// (token, head) row (wave w merges the 16-split blocks w, w + 16, ... and
-// wave 0 merges the 16 results in a fixed order). Otherwise one wave per row.
+// Few rows with many splits (shared_rows): up to 512 splits, a work-group of
+// 16 waves per (token, head) row and 32 of its columns (wave w merges split
+// block w, wave 0 merges the 16 results in a fixed order); beyond 512, one
+// work-group per row (wave w merges the 16-split blocks w, w + 16, ...).
+// Otherwise one wave per row.
 // The kernels are latency-bound, so the loads are ordered by round: the
 // padding bound, the split-count marker and the wave's LSEs are issued
 // together (the LSEs before their count is known; slots past it are then
@@ -356,13 +358,12 @@ __global__ __launch_bounds__(256) void combine_splits(const CombineParams c) {
   write_row<NC>(c, tok, head, M, num, den, lane);
 }
 
-// Few rows with many splits (shared_rows): a work-group of 16 waves per row;
-// wave w merges the kBlk-split blocks w, w + 16, ... (one round of loads for
-// up to 16 kBlk splits) and wave 0 merges the 16 results in a fixed order.
-// kBlk is 16, or 32 for 257 to 512 splits (one block per wave: one
-// speculative round of LSE loads instead of a max pass and a pass per
-// block). Beyond 512 the workspace is an upper bound and a row's live splits
-// are often few, which 16-split blocks spread over more waves.
+// Few rows with more than 512 splits (shared_rows): a work-group of 16 waves
+// per row; wave w merges the 16-split blocks w, w + 16, ... and wave 0 merges
+// the 16 results in a fixed order. Beyond 512 the workspace is an upper bound
+// and a row's live splits are often few (config 1: 32 of 2048), which
+// 16-split blocks spread over more waves. (Up to 512 splits, combine_cols
+// below.)
 constexpr int kSharedWaves = 16;
 
 template <int D, int kSharedBlock>
@@ -424,6 +425,102 @@ __global__ __launch_bounds__(kSharedWaves * 64) void combine_shared(const Combin
   write_row<NC>(c, tok, head, Mg, ng, dg, lane);
 }
 
+// Few rows with up to 16 kBlk splits each, split by columns as well: a
+// work-group of 16 waves per (row, 32 columns), so a row's partials are read
+// by D / 32 compute units instead of one (config 3's 32 rows then use 128
+// compute units, the D = 256 decode's 12 rows 96). Wave w merges the splits
+// of block w, two splits per load instruction (lanes 0-31 split 2k, lanes
+// 32-63 split 2k + 1, one column each), the two halves are added, and wave 0
+// merges the 16 waves in a fixed order. Loads are ordered by round as in
+// combine_shared: the marker, the padding bound, the wave's LSEs and all its
+// partial columns in one round.
+constexpr int kColsPerPart = 32;
+
+template <int D, int kBlk>
+__global__ __launch_bounds__(kSharedWaves * 64) void combine_cols(const CombineParams c) {
+  constexpr int kParts = D / kColsPerPart;
+  constexpr int kLd = kBlk / 2;  // partial loads per lane
+  __shared__ float part_m[kSharedWaves], part_den[kSharedWaves];
+  __shared__ float part_num[kSharedWaves][kColsPerPart];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t row = blockIdx.x / kParts;
+  const int part = static_cast<int>(blockIdx.x - row * kParts);
+  const int64_t tok = row / c.num_q_heads;
+  const int head = static_cast<int>(row - tok * c.num_q_heads);
+  if (tok >= c.num_tokens) return;  // uniform over the work-group
+  const int bound = ld_ro(c.qsl, c.num_reqs);
+  const uint32_t bits = marker_bits(c, tok, head);  // read on every path: the slot exists
+  const float x_spec = lse_slot<kBlk>(c, tok, head, wave, lane);
+  const int half = lane >> 5;
+  const int col = kColsPerPart * part + (lane & 31);
+  const char* o_col =
+      c.ws_o + tok * c.s_wo_tok + static_cast<int64_t>(head) * c.s_wo_head + 4 * col;
+  const int s0 = kBlk * wave;
+  float ov[kLd];
+#pragma unroll
+  for (int k = 0; k < kLd; ++k) {
+    const int s = s0 + 2 * k + half;
+    ov[k] = s < c.num_splits
+                ? *reinterpret_cast<const float*>(o_col + static_cast<int64_t>(s) * c.s_wo_split)
+                : 0.0f;
+  }
+  if (tok >= bound) return;  // padding row, uniform over the work-group
+  const int S = c.seq_lens != nullptr ? splits_of_marker(c, bits) : c.num_splits;
+  if (c.seq_lens != nullptr && S == 1) return;  // written to out by the attention kernel
+  const float x = lane < kBlk && s0 + lane < S ? x_spec : kNegInf;
+  const float M = wave_max(x > kNegInf ? x : kNegInf);  // NaN never wins
+  float num = 0.0f, den = 0.0f;
+  if (M > kNegInf) {
+    const float w_l = x > kNegInf ? __builtin_amdgcn_exp2f(x - M) : 0.0f;
+#pragma unroll
+    for (int k = 0; k < kLd; ++k) {
+      const float wa = __builtin_bit_cast(
+          float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w_l), 2 * k));
+      const float wb = __builtin_bit_cast(
+          float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w_l), 2 * k + 1));
+      const float w = half ? wb : wa;
+      if (w > 0.0f) num = fmaf(w, ov[k], num);
+    }
+    den = wave_sum(w_l);
+  }
+  num += __shfl_xor(num, 32);  // the two halves of the column (commutative)
+  if (lane == 0) {
+    part_m[wave] = M;
+    part_den[wave] = den;
+  }
+  if (lane < kColsPerPart) part_num[wave][lane] = num;
+  __syncthreads();
+  if (wave != 0 || lane >= kColsPerPart) return;
+  float Mg = kNegInf;
+#pragma unroll
+  for (int w = 0; w < kSharedWaves; ++w) Mg = part_m[w] > Mg ? part_m[w] : Mg;
+  float ng = 0.0f, dg = 0.0f;
+  if (Mg > kNegInf) {
+#pragma unroll
+    for (int w = 0; w < kSharedWaves; ++w) {
+      if (part_m[w] > kNegInf) {
+        const float a = __builtin_amdgcn_exp2f(part_m[w] - Mg);
+        ng = fmaf(a, part_num[w][lane], ng);
+        dg = fmaf(a, part_den[w], dg);
+      }
+    }
+  }
+  const float r = dg > 0.0f ? ng * (1.0f / dg) : 0.0f;
+  char* dst = c.out + tok * c.s_out_tok + static_cast<int64_t>(head) * c.s_out_head;
+  if (c.out_dtype == PTH_ATTN_BF16)
+    *reinterpret_cast<__bf16*>(dst + 2 * col) = static_cast<__bf16>(r);
+  else if (c.out_dtype == PTH_ATTN_F16)
+    *reinterpret_cast<_Float16*>(dst + 2 * col) = static_cast<_Float16>(r);
+  else
+    *reinterpret_cast<float*>(dst + 4 * col) = r;
+  if (c.lse_out != nullptr && part == 0 && lane == 0) {
+    float* lo = reinterpret_cast<float*>(reinterpret_cast<char*>(c.lse_out) + tok * c.s_lo_tok +
+                                         static_cast<int64_t>(head) * c.s_lo_head);
+    *lo = dg > 0.0f ? (Mg + __builtin_amdgcn_logf(dg)) * 0.69314718055994530942f : kNegInf;
+  }
+}
+
 // -inf into the log2-LSE slot of every split s >= live of every query row
 // (live: the splits the attention kernel wrote for the row), so that a
 // combine over all num_splits splits ignores them, as the reference's launch
@@ -446,8 +543,12 @@ __global__ __launch_bounds__(256) void fill_unused_splits(const CombineParams c)
 
 template <int D>
 void launch_combine_d(const CombineParams& c, int64_t rows, hipStream_t stream) {
-  if (c.shared_rows && c.num_splits > kSharedWaves * 16 && c.num_splits <= kSharedWaves * 32)
-    hipLaunchKernelGGL((combine_shared<D, 32>), dim3(static_cast<unsigned>(rows)),
+  const unsigned parts = static_cast<unsigned>(D / kColsPerPart);
+  if (c.shared_rows && c.num_splits <= kSharedWaves * 16)
+    hipLaunchKernelGGL((combine_cols<D, 16>), dim3(static_cast<unsigned>(rows) * parts),
+                       dim3(kSharedWaves * 64), 0, stream, c);
+  else if (c.shared_rows && c.num_splits <= kSharedWaves * 32)
+    hipLaunchKernelGGL((combine_cols<D, 32>), dim3(static_cast<unsigned>(rows) * parts),
                        dim3(kSharedWaves * 64), 0, stream, c);
   else if (c.shared_rows)
     hipLaunchKernelGGL((combine_shared<D, 16>), dim3(static_cast<unsigned>(rows)),

@@ -375,6 +375,22 @@ def test_out_dtypes(dtype):
         assert_parity(compare(out, lse, ref_out, ref_lse, valid), name=c.name, strict=False)
 
 
+# The column-split combine (few rows, 65 to 512 splits: a work-group per row
+# and 32 columns) for every head size and output dtype, with the LSE.
+@pytest.mark.parametrize("D", [64, 128, 256])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("S", [200, 480])
+def test_combine_column_parts(D, dtype, S):
+    Hq, Hkv = (12, 2) if D == 256 else (8, 2)
+    c = Case(f"cols-d{D}", q_lens=[1, 2], seq_lens=[40000, 3000], Hq=Hq, Hkv=Hkv, D=D, seed=31)
+    b = materialize(c, DEV)
+    out, lse = run_capi(b, num_splits=S, out_dtype=dtype)
+    ref_out, ref_lse, valid = oracle_of(b)
+    res = compare(out, lse, ref_out, ref_lse, valid)
+    print(f"  D={D} {dtype} S={S} -> {res}", flush=True)
+    assert_parity(res, name=f"cols D={D} {dtype} S={S}", strict=False)
+
+
 # ---------------------------------------------------------------- op surface
 def test_op_equals_capi_bitwise():
     """The torch op and the C ABI run the same launcher: identical bytes."""
