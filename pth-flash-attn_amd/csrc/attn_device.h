@@ -303,7 +303,7 @@ struct Work {
       else per = stream_per(d, lane, total);
       wg = (w / p.gu) * static_cast<int>(gridDim.x) + static_cast<int>(blockIdx.x);
       wave = w % p.gu;
-      pos = static_cast<int64_t>(wg) * per;
+      pos = static_cast<int64_t>(wg) * per + kStreamStartPositions;
       stop = pos + per < total ? pos + per : total;
     } else {
       next_u = blockIdx.x * kGroupUnits + w;

@@ -202,7 +202,9 @@ PA_HD int32_t request_row_tiles(int32_t q_len, int32_t bq) {
 // 32-aligned base, are a stream of 32-key chunks; the streams of all
 // (request, row tile, group of 8 KV-head units) are laid end to end, in that
 // order, each preceded by kStreamStartPositions positions that hold no chunk,
-// and work-group b of the grid takes positions [b per, (b + 1) per). A stream
+// and work-group b of the grid takes positions [b per + kStreamStartPositions,
+// (b + 1) per + kStreamStartPositions) (the first stream's start positions
+// are every work-group's own first start, so no range holds them). A stream
 // cut by such a boundary is computed in parts (its splits), one per
 // work-group whose range meets its chunks, and merged by the LSE combine.
 // The start positions price what a wave pays to begin a unit (its
@@ -247,7 +249,8 @@ PA_HD void request_spans(int32_t q_len, int32_t seq_len, int32_t bq, int32_t win
   }
 }
 
-// Stream positions per work-group: an even share of the `total` positions,
+// Stream positions per work-group: an even share of the `total` positions
+// (less the first stream's start positions, which no range holds),
 // but at least kMinChunksPerSplit and enough that no stream of up to `max_n`
 // chunks meets more than num_splits work-groups (n consecutive chunk
 // positions meet at most ceil((n - 1) / per) + 1 of them). One chunk is the floor: a small launch
@@ -256,7 +259,8 @@ PA_HD void request_spans(int32_t q_len, int32_t seq_len, int32_t bq, int32_t win
 // with 1; long launches have shares far above the floor).
 constexpr int32_t kMinChunksPerSplit = 1;
 PA_HD int64_t chunks_per_group(int64_t total, int32_t max_n, int32_t num_wg, int32_t num_splits) {
-  int64_t per = (total + num_wg - 1) / num_wg;
+  const int64_t ranged = total > kStreamStartPositions ? total - kStreamStartPositions : 0;
+  int64_t per = (ranged + num_wg - 1) / num_wg;
   if (per < kMinChunksPerSplit) per = kMinChunksPerSplit;
   if (num_splits > 1 && max_n > 1) {
     const int64_t need = (static_cast<int64_t>(max_n) - 1 + num_splits - 2) / (num_splits - 1);
@@ -266,13 +270,12 @@ PA_HD int64_t chunks_per_group(int64_t total, int32_t max_n, int32_t num_wg, int
 }
 
 // The work-groups whose ranges meet the chunks of the stream of n chunks
-// that starts at position c0 (its chunks at [c0 + kStreamStartPositions,
-// + n)): first and count (its splits); split s of the stream is work-group
-// first + s.
+// that starts at position c0: first and count (its splits); split s of the
+// stream is work-group first + s. (Its chunks lie at [c0 + start, c0 + start
+// + n) and range b starts at b per + start, so the start cancels.)
 PA_HD void stream_splits(int64_t c0, int32_t n, int64_t per, int32_t& first, int32_t& live) {
-  const int64_t cs = c0 + kStreamStartPositions;
-  first = static_cast<int32_t>(cs / per);
-  live = n > 0 ? static_cast<int32_t>((cs + n - 1) / per) - first + 1 : 1;
+  first = static_cast<int32_t>(c0 / per);
+  live = n > 0 ? static_cast<int32_t>((c0 + n - 1) / per) - first + 1 : 1;
 }
 
 }  // namespace pa

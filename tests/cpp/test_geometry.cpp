@@ -167,7 +167,8 @@ static void streams() {
     const int num_wg = 1 + rng() % 300;
     const int S = 2 + rng() % 300;
     const int64_t per = chunks_per_group(total, mx, num_wg, S);
-    CHECK(per >= kMinChunksPerSplit && per * num_wg >= total, "per covers the total");
+    CHECK(per >= kMinChunksPerSplit && per * num_wg + kStreamStartPositions >= total,
+          "per covers the total");
     // Per work-group: its chunks plus kStreamStartPositions per unit (a
     // stream whose chunks its range meets) never exceed per plus one start.
     std::vector<int64_t> cost(num_wg, 0);
@@ -181,7 +182,7 @@ static void streams() {
       const int64_t cs = c0 + kStreamStartPositions;
       int bf_first = -1, bf_count = 0;
       for (int b = 0; b < num_wg; ++b) {
-        const int64_t lo = b * per, hi = lo + per;
+        const int64_t lo = b * per + kStreamStartPositions, hi = lo + per;
         if (lo < cs + n && hi > cs) {
           if (bf_first < 0) bf_first = b;
           ++bf_count;
