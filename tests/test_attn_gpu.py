@@ -442,6 +442,50 @@ def test_public_entry_points_windowed_verify(S, causal):
     assert_parity(res, name=f"public window S={S}", strict=False)
 
 
+# ------------------------------------- split launches of more than 64 requests
+# The split partition reads the requests 64 at a time (one lane each): with
+# more than 64 the partition is sized over several windows, a wave's stream
+# lies in a later window than the first (the cursor refills), and the combine
+# and the unused-split fill locate their rows the same way. Every kernel
+# family that splits: page-row decode and verify (8 KV heads), the staged
+# kernel (2 KV heads), the register-load kernel (windowed verify), and the
+# D = 256 / D = 64 kernels.
+GRID_MANY = [
+    Case("many-decode", q_lens=[1] * 150, seq_lens=uniform_lengths(150, 1, 3000, 7), seed=80),
+    Case("many-decode-g4", q_lens=[1] * 200, seq_lens=uniform_lengths(200, 1, 1200, 8),
+         Hq=8, Hkv=2, seed=81),
+    Case("many-verify-q4", q_lens=[4] * 130, seq_lens=uniform_lengths(130, 4, 2500, 9), seed=82),
+    Case("many-window-q16", q_lens=[16] * 100, seq_lens=uniform_lengths(100, 16, 5000, 10),
+         window=256, seed=83),
+    Case("many-ragged", q_lens=[1, 3, 1, 2] * 33, seq_lens=uniform_lengths(132, 3, 1500, 13),
+         Hq=16, Hkv=4, block_size=32, layout="HND", seed=84),
+    Case("many-d256", q_lens=[1] * 90, seq_lens=uniform_lengths(90, 1, 2000, 11), Hq=16, Hkv=2,
+         D=256, seed=85),
+    Case("many-d64", q_lens=[1] * 90, seq_lens=uniform_lengths(90, 1, 2000, 12), Hq=16, Hkv=2,
+         D=64, seed=86),
+]
+
+
+@pytest.mark.parametrize("case", GRID_MANY, ids=lambda c: c.name)
+def test_many_requests_split(case):
+    assert len(case.q_lens) > 64 and case.plan().num_splits > 1
+    check_case(case)
+
+
+@pytest.mark.parametrize("S", [3, 37])
+@pytest.mark.parametrize("idx", [0, 2, 3], ids=["decode", "verify", "window"])
+def test_many_requests_public_entry_points(idx, S):
+    """More than 64 requests through pth_attn_attention then pth_attn_combine
+    over all S splits: the unused-split fill must cover every request window."""
+    c = GRID_MANY[idx]
+    b = materialize(c, DEV)
+    out, _ = run_capi(b, num_splits=S, with_lse=False)
+    ref_out, ref_lse, valid = oracle_of(b)
+    res = compare(out, None, ref_out, ref_lse, valid)
+    print(f"  {c.name} S={S} -> {res}", flush=True)
+    assert_parity(res, name=f"{c.name} public S={S}", strict=False)
+
+
 # ------------------------------------------------- page-row integer QK
 @pytest.mark.parametrize("q_dtype", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
 @pytest.mark.parametrize("S", [1, None], ids=["S1", "plan"])
