@@ -36,19 +36,40 @@ STEPS = [
 ]
 
 
+# Bits of a quiet NaN that no kernel writes: every float of the reserved
+# buffer starts with it, and those outside the views the launches were given
+# (the reservation's unused tail and a guard after each region) must keep it.
+CANARY = 0x7FBADBAD
+GUARD = 4096  # floats after each region
+
+
 def _workspace(builder: slices.SliceBuilder, Hq: int, D: int):
+    """The reservation the builder sized (o partials, guard, LSE partials,
+    guard), handed out as views from the start of each region, as vLLM's
+    workspace manager does; returns (provide, asked, check)."""
     o_shape, lse_shape = planner.workspace_shapes(ws_token_splits=builder.ws_token_splits, Hq=Hq, D=D)
-    n_o = math.prod(o_shape)
-    buf = torch.empty(n_o + math.prod(lse_shape), dtype=torch.float32, device=DEV)
+    n_o, n_l = math.prod(o_shape), math.prod(lse_shape)
+    l0 = n_o + GUARD
+    buf = torch.full((l0 + n_l + GUARD,), CANARY, dtype=torch.int32, device=DEV).view(torch.float32)
     asked = []
 
     def provide(o, lse):
         asked.append((o, lse))
         no, nl = math.prod(o), math.prod(lse)
-        assert no <= n_o and nl <= math.prod(lse_shape), "launch beyond the reservation"
-        return buf[:no].view(o), buf[n_o:n_o + nl].view(lse)
+        assert no <= n_o and nl <= n_l, "launch beyond the reservation"
+        return buf[:no].view(o), buf[l0:l0 + nl].view(lse)
 
-    return provide, asked
+    def check():
+        """Floats outside every view handed out still hold the canary."""
+        used_o = max((math.prod(o) for o, _ in asked), default=0)
+        used_l = max((math.prod(lse) for _, lse in asked), default=0)
+        bits = buf.view(torch.int32)
+        for lo, hi in ((used_o, l0), (l0 + used_l, bits.numel())):
+            bad = int((bits[lo:hi] != CANARY).sum())
+            assert bad == 0, f"{bad} floats written outside the workspace views in [{lo}, {hi})"
+        return used_o, used_l
+
+    return provide, asked, check
 
 
 @pytest.mark.parametrize("name,Hq,Hkv,D,k,window,causal,q_lens,seq_lens", STEPS,
@@ -73,7 +94,7 @@ def test_step_slices_match_the_oracle(name, Hq, Hkv, D, k, window, causal, q_len
         query_start_loc=qsl, query_start_loc_cpu=qsl.cpu(), seq_lens=cache.seq_lens,
         block_table=cache.block_table, num_reqs=len(q_lens), num_actual_tokens=q.shape[0],
         max_query_len=max(q_lens), causal=causal)
-    provide, asked = _workspace(builder, Hq, D)
+    provide, asked, check = _workspace(builder, Hq, D)
     none = torch.empty(0, dtype=torch.float32, device=DEV)
     slices.run_slices(step, query=q, output=out, caches=views, scale=1.0 / math.sqrt(D),
                       window=window, workspace=provide, no_workspace=none,
@@ -82,6 +103,9 @@ def test_step_slices_match_the_oracle(name, Hq, Hkv, D, k, window, causal, q_len
     parts = [p for p in (step.decode, step.prefill) if p is not None]
     print(f"  slices: {[(p.token_start, p.token_end, p.plan.num_splits) for p in parts]}", flush=True)
     assert len(parts) >= 1 and not torch.isnan(out.float()).any()
+    used = check()
+    print(f"  workspace: {used} floats of ({builder.ws_token_splits} token-splits) used, "
+          f"canaries intact", flush=True)
 
     case = Case(name, q_lens=list(q_lens), seq_lens=list(seq_lens), Hq=Hq, Hkv=Hkv, D=D,
                 window=window, causal=causal, layout="HND")
