@@ -606,3 +606,44 @@ def test_config5_mixed_sampled():
         res = compare(out, lse, ref_out, ref_lse, v)
         print(f"  rows [{lo}, {hi}) -> {res}", flush=True)
         assert_parity(res, name=f"cfg5 rows {lo}:{hi}", strict=True)
+
+
+# ------------------------------------------------- long prefill chunks
+# The reference's prefill tests (tests/gpu/test_attn_prefill.py) run q = 2048
+# and q = 8192 behind a prefix and check sampled windows of whole row tiles
+# (fp64 over a whole 8192-token request would take minutes) plus finiteness
+# of the whole output. Same here, on the row-block kernel (D = 128) and the
+# D = 256 kernels.
+LONG_PREFILL = [
+    Case("prefill-8192-prefix", q_lens=[8192, 1], seq_lens=[16384, 5000], is_prefill=True,
+         seed=70),
+    Case("prefill-8192-window", q_lens=[8192], seq_lens=[12000], window=4096, is_prefill=True,
+         seed=71),
+    Case("prefill-4096-d256", q_lens=[4096, 3], seq_lens=[6000, 3], Hq=12, Hkv=2, D=256,
+         is_prefill=True, seed=72),
+]
+
+
+@pytest.mark.parametrize("case", LONG_PREFILL, ids=lambda c: c.name)
+def test_long_prefill_sampled(case):
+    import oracle
+    print(f"case {case.name}: S={case.plan().num_splits} wm={case.plan().wm}", flush=True)
+    b = materialize(case, DEV)
+    out, lse = run_capi(b)
+    q0 = case.q_lens[0]
+    assert torch.isfinite(out[:sum(case.q_lens)].float()).all(), "non-finite output"
+    hb = Batch(case, b.cache.to("cpu"), b.q.cpu(), b.qsl.cpu())
+    args = launch_args(hb, torch.empty(hb.q.shape, dtype=torch.float32), num_splits=1, bq=1)
+    T = case.T
+    # 16-row tiles at the chunk's start, its end and six points between, then
+    # the other requests' rows.
+    sample = [(t, t + 16) for t in np.linspace(0, q0 - 16, 8).astype(int).tolist()]
+    if T > q0:
+        sample.append((q0, T))
+    for lo, hi in sample:
+        ref_out, ref_lse, valid = oracle.attention(args, threads=16, rows=(lo, hi))
+        v = np.zeros(T, dtype=bool)
+        v[lo:hi] = valid[lo:hi]
+        res = compare(out, lse, ref_out, ref_lse, v)
+        print(f"  rows [{lo}, {hi}) -> {res}", flush=True)
+        assert_parity(res, name=f"{case.name} rows {lo}:{hi}", strict=False)
