@@ -46,17 +46,36 @@ constexpr float kNegInf = -__builtin_inff();
 template <int NC>
 constexpr int kBatch = 32 / NC;
 
-__device__ __forceinline__ float wave_max(float x) {
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) x = fmaxf(x, __shfl_xor(x, d));
-  return x;
+template <int kCtrl>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __builtin_bit_cast(float, dpp_i32<kCtrl>(__builtin_bit_cast(int, v)));
 }
-// Butterfly sum: every lane adds the same pairs (commutatively), so all lanes
-// hold the same, order-fixed total.
+// Maximum over the 64 lanes (every lane; DPP within rows of 16 lanes, then
+// the four row maxima).
+__device__ __forceinline__ float wave_max(float x) {
+  x = fmaxf(x, dpp_f32<0xB1>(x));   // quad_perm [1, 0, 3, 2]
+  x = fmaxf(x, dpp_f32<0x4E>(x));   // quad_perm [2, 3, 0, 1]
+  x = fmaxf(x, dpp_f32<0x141>(x));  // row_half_mirror
+  x = fmaxf(x, dpp_f32<0x140>(x));  // row_mirror
+  auto lane_f = [&](int l) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), l));
+  };
+  return fmaxf(fmaxf(lane_f(0), lane_f(16)), fmaxf(lane_f(32), lane_f(48)));
+}
+// Butterfly sum: within each row of 16 lanes every lane adds the same pairs
+// (commutatively; quad swaps, then half-row and row mirrors pair the quad and
+// half-row sums), then the row sums as (r0 + r1) + (r2 + r3) -- the pairing
+// of a butterfly over lane distances 1, 2, ..., 32, so every lane holds the
+// same, order-fixed total.
 __device__ __forceinline__ float wave_sum(float x) {
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) x += __shfl_xor(x, d);
-  return x;
+  x += dpp_f32<0xB1>(x);   // quad_perm [1, 0, 3, 2]
+  x += dpp_f32<0x4E>(x);   // quad_perm [2, 3, 0, 1]
+  x += dpp_f32<0x141>(x);  // row_half_mirror
+  x += dpp_f32<0x140>(x);  // row_mirror
+  auto lane_f = [&](int l) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), l));
+  };
+  return (lane_f(0) + lane_f(16)) + (lane_f(32) + lane_f(48));
 }
 
 // Request of token tok: the number of requests that end at or before it

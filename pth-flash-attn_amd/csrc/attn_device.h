@@ -351,12 +351,7 @@ struct Work {
         const int r = r0 + lane;
         const int units =
             r < p.num_reqs ? request_row_tiles(p.qsl[r + 1] - p.qsl[r], p.bq) * p.n_hu : 0;
-        int x = units;
-#pragma unroll
-        for (int dd = 1; dd < 64; dd <<= 1) {
-          const int v = __shfl_up(x, dd);
-          if (lane >= dd) x += v;
-        }
+        const int x = wave_scan32(units);
         incl = x;
         u1 = u0 + __builtin_amdgcn_readlane(x, 63);
       }

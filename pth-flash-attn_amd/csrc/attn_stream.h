@@ -42,8 +42,34 @@ __device__ __forceinline__ int64_t readlane64(int64_t x, int l) {
   return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
 }
 
-// Inclusive prefix sum over the 64 lanes.
+// Wave-wide reductions by DPP lane moves (register to register, a few
+// cycles each) instead of __shfl (ds_bpermute: an LDS crossbar round trip of
+// ~100 cycles, and a chain of them sat on every work-group's start path).
+template <int kCtrl, int kRowMask = 0xf>
+__device__ __forceinline__ int dpp_i32(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, kCtrl, kRowMask, 0xf, true);
+}
+
+// Inclusive prefix sum over the 64 lanes: within each row of 16 lanes by
+// row shifts of 1, 2, 4 and 8 (lanes shifted in from outside the row add 0),
+// then lane 15's running total into rows 1 and 3 and lane 31's into rows 2
+// and 3 (row broadcasts).
+__device__ __forceinline__ int32_t wave_scan32(int32_t x) {
+  x += dpp_i32<0x111>(x);       // row_shr:1
+  x += dpp_i32<0x112>(x);       // row_shr:2
+  x += dpp_i32<0x114>(x);       // row_shr:4
+  x += dpp_i32<0x118>(x);       // row_shr:8
+  x += dpp_i32<0x142, 0xa>(x);  // row_bcast:15 (rows 1, 3)
+  x += dpp_i32<0x143, 0xc>(x);  // row_bcast:31 (rows 2, 3)
+  return x;
+}
+
+// Inclusive prefix sum over the 64 lanes. Values in [0, 2^24) (stream
+// positions of one request, always in practice) take the 32-bit DPP scan;
+// otherwise a 64-bit shift-up scan.
 __device__ __forceinline__ int64_t wave_scan64(int64_t x, int lane) {
+  if (__ballot(static_cast<uint64_t>(x) >= (1u << 24)) == 0)
+    return wave_scan32(static_cast<int32_t>(x));
 #pragma unroll
   for (int d = 1; d < 64; d <<= 1) {
     const int64_t v = __shfl_up(x, d);
@@ -52,13 +78,16 @@ __device__ __forceinline__ int64_t wave_scan64(int64_t x, int lane) {
   return x;
 }
 
+// Maximum over the 64 lanes (every lane): a butterfly within each row of 16
+// lanes (quad swaps, half-row and row mirrors), then the four row maxima.
 __device__ __forceinline__ int32_t wave_max32(int32_t x) {
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const int32_t v = __shfl_xor(x, d);
-    x = v > x ? v : x;
-  }
-  return x;
+  x = max(x, dpp_i32<0xB1>(x));   // quad_perm [1, 0, 3, 2]
+  x = max(x, dpp_i32<0x4E>(x));   // quad_perm [2, 3, 0, 1]
+  x = max(x, dpp_i32<0x141>(x));  // row_half_mirror
+  x = max(x, dpp_i32<0x140>(x));  // row_mirror
+  const int32_t a = max(__builtin_amdgcn_readlane(x, 0), __builtin_amdgcn_readlane(x, 16));
+  const int32_t b = max(__builtin_amdgcn_readlane(x, 32), __builtin_amdgcn_readlane(x, 48));
+  return max(a, b);
 }
 
 // Stream positions of request r (all its row tiles and groups) and the chunk
