@@ -118,8 +118,9 @@ __device__ __forceinline__ void reg_load(const AttnParams& p, const RegLoader& R
 
 template <bool kWindow, bool kStream, bool kF16Q>
 __global__ __launch_bounds__(kFwdWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
-void attn_fwd_paged_reg(const AttnParams p) {
+void attn_fwd_paged_reg(const AttnParams p_arg) {
   const int lane = threadIdx.x & 63;
+  const AttnParams p = params_in_registers(p_arg, lane);
   const float scl = scale_factor(lane & 15, p.scale_log2);
   Work<kWindow, kStream> work;
   work.init(p, lane);

@@ -112,11 +112,12 @@ __device__ __forceinline__ void load_chunk_d(const AttnParams& p, const Unit& U,
 
 template <bool kWindow, bool kStream, bool kF16Q, int D>
 __global__ __launch_bounds__(kFwdWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
-void attn_fwd_generic(const AttnParams p) {
+void attn_fwd_generic(const AttnParams p_arg) {
   // Two chunks in registers (one loading while the other is computed) while
   // they fit: 2 x 65 VGPRs at D = 256 do not, so D = 256 loads in turn.
   constexpr bool kDouble = D <= 128;
   const int lane = threadIdx.x & 63;
+  const AttnParams p = params_in_registers(p_arg, lane);
   const float scl = scale_factor(lane & 15, p.scale_log2);
   Work<kWindow, kStream> work;
   work.init(p, lane);
@@ -294,10 +295,11 @@ __device__ __forceinline__ void read256(uint32_t slot, int lane, ChunkD<256>& ch
 
 template <bool kStream, bool kF16Q>
 __global__ __launch_bounds__(kFwdWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
-void attn_fwd_paged256(const AttnParams p) {
+void attn_fwd_paged256(const AttnParams p_arg) {
   constexpr int D = 256;
   __shared__ __attribute__((aligned(16))) char lds_all[kFwdWaves * kSlot256Bytes];
   const int lane = threadIdx.x & 63;
+  const AttnParams p = params_in_registers(p_arg, lane);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   char* slot = lds_all + wave * kSlot256Bytes;
   const uint32_t slot_a = lds_offset(slot);

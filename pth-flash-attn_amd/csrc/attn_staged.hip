@@ -183,9 +183,10 @@ __device__ __forceinline__ bool next_live_unit(const AttnParams& p, Work<kWindow
 
 template <bool kWindow, bool kStream, bool kF16Q>
 __global__ __launch_bounds__(kFwdWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
-void attn_fwd_staged(const AttnParams p) {
+void attn_fwd_staged(const AttnParams p_arg) {
   __shared__ __attribute__((aligned(16))) char lds_all[kFwdWaves * kSlotBytes];
   const int lane = threadIdx.x & 63;
+  const AttnParams p = params_in_registers(p_arg, lane);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   char* slot = lds_all + wave * kSlotBytes;
   const ReadOffsets ro = read_offsets(lane);

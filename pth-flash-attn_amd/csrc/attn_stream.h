@@ -15,6 +15,30 @@
 
 namespace pa {
 
+// A kernel's launch parameters as values: the kernel argument is read at
+// kernel entry by one vector load per lane (dword i of the argument segment
+// in lane i % 64 of one of two registers: one memory round trip), and every
+// field is taken from those registers by a lane read. Left to itself, the
+// compiler reads the argument segment with scalar loads near each use and,
+// under scalar-register pressure, reads fields again later: several
+// dependent memory round trips on every wave's way to its first chunk.
+template <class Params>
+__device__ __forceinline__ Params params_in_registers(const Params& a, int lane) {
+  static_assert(sizeof(Params) % 4 == 0, "dword-sized parameters");
+  constexpr int kWords = static_cast<int>(sizeof(Params) / 4);
+  static_assert(kWords <= 128, "parameters fit two registers of 64 lanes");
+  const uint32_t* src = reinterpret_cast<const uint32_t*>(&a);
+  uint32_t v0 = lane < kWords ? src[lane] : 0u;
+  uint32_t v1 = lane + 64 < kWords ? src[lane + 64] : 0u;
+  asm volatile("" : "+v"(v0), "+v"(v1));
+  uint32_t w[kWords];
+#pragma unroll
+  for (int i = 0; i < kWords; ++i) w[i] = __builtin_amdgcn_readlane(i < 64 ? v0 : v1, i & 63);
+  Params r;
+  __builtin_memcpy(&r, w, sizeof(w));
+  return r;
+}
+
 // Read-only inputs (query_start_loc, seq_lens, block_table) are read through
 // the constant address space: a wave-uniform index then becomes a scalar
 // load, which is tracked by lgkmcnt and never makes the wave wait for its
