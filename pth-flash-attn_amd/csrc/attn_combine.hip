@@ -365,6 +365,9 @@ __global__ __launch_bounds__(256) void combine_splits(const CombineParams c) {
   constexpr int kSpec = 4;  // many rows, few live splits each
   float ov_spec[kSpec][NC];
   spec_rows<NC, 64, kSpec>(c, tok, head, 0, lane, ov_spec);
+  // One round: the compiler would otherwise issue the marker load only after
+  // the padding-bound test below (a second dependent round trip).
+  asm volatile("" ::"s"(bits), "s"(bound) : "memory");
   if (tok >= bound) return;  // padding row
   const int S = c.seq_lens != nullptr ? splits_of_marker(c, bits) : c.num_splits;
   if (c.seq_lens != nullptr && S == 1) return;  // written to out by the attention kernel
@@ -405,6 +408,9 @@ __global__ __launch_bounds__(kSharedWaves * 64) void combine_shared(const Combin
   constexpr int kSpec = kOneBatch<NC, kSharedBlock>;  // few rows, many splits each
   float ov_spec[kSpec][NC];
   spec_rows<NC, kSharedBlock, kSpec>(c, tok, head, wave, lane, ov_spec);
+  // One round: the compiler would otherwise issue the marker load only after
+  // the padding-bound test below (a second dependent round trip).
+  asm volatile("" ::"s"(bits), "s"(bound) : "memory");
   if (tok >= bound) return;  // padding row, uniform over the work-group
   const int S = c.seq_lens != nullptr ? splits_of_marker(c, bits) : c.num_splits;
   if (c.seq_lens != nullptr && S == 1) return;  // written to out by the attention kernel
@@ -423,9 +429,19 @@ __global__ __launch_bounds__(kSharedWaves * 64) void combine_shared(const Combin
   for (int i = 0; i < NC; ++i) part_num[wave][i][lane] = num[i];
   __syncthreads();
   if (wave != 0) return;
+  // Every wave's result read at once (one LDS round trip), then merged in
+  // wave order.
+  float pm[kSharedWaves], pd[kSharedWaves], pn[kSharedWaves][NC];
+#pragma unroll
+  for (int w = 0; w < kSharedWaves; ++w) {
+    pm[w] = part_m[w];
+    pd[w] = part_den[w];
+#pragma unroll
+    for (int i = 0; i < NC; ++i) pn[w][i] = part_num[w][i][lane];
+  }
   float Mg = kNegInf;
 #pragma unroll
-  for (int w = 0; w < kSharedWaves; ++w) Mg = part_m[w] > Mg ? part_m[w] : Mg;
+  for (int w = 0; w < kSharedWaves; ++w) Mg = pm[w] > Mg ? pm[w] : Mg;
   float ng[NC];
 #pragma unroll
   for (int i = 0; i < NC; ++i) ng[i] = 0.0f;
@@ -433,11 +449,11 @@ __global__ __launch_bounds__(kSharedWaves * 64) void combine_shared(const Combin
   if (Mg > kNegInf) {
 #pragma unroll
     for (int w = 0; w < kSharedWaves; ++w) {
-      if (part_m[w] > kNegInf) {
-        const float a = __builtin_amdgcn_exp2f(part_m[w] - Mg);
+      if (pm[w] > kNegInf) {
+        const float a = __builtin_amdgcn_exp2f(pm[w] - Mg);
 #pragma unroll
-        for (int i = 0; i < NC; ++i) ng[i] = fmaf(a, part_num[w][i][lane], ng[i]);
-        dg = fmaf(a, part_den[w], dg);
+        for (int i = 0; i < NC; ++i) ng[i] = fmaf(a, pn[w][i], ng[i]);
+        dg = fmaf(a, pd[w], dg);
       }
     }
   }
@@ -484,6 +500,9 @@ __global__ __launch_bounds__(kSharedWaves * 64) void combine_cols(const CombineP
                 ? *reinterpret_cast<const float*>(o_col + static_cast<int64_t>(s) * c.s_wo_split)
                 : 0.0f;
   }
+  // One round: the compiler would otherwise issue the marker load only after
+  // the padding-bound test below (a second dependent round trip).
+  asm volatile("" ::"s"(bits), "s"(bound) : "memory");
   if (tok >= bound) return;  // padding row, uniform over the work-group
   const int S = c.seq_lens != nullptr ? splits_of_marker(c, bits) : c.num_splits;
   if (c.seq_lens != nullptr && S == 1) return;  // written to out by the attention kernel
@@ -511,17 +530,26 @@ __global__ __launch_bounds__(kSharedWaves * 64) void combine_cols(const CombineP
   if (lane < kColsPerPart) part_num[wave][lane] = num;
   __syncthreads();
   if (wave != 0 || lane >= kColsPerPart) return;
+  // Every wave's result read at once (one LDS round trip), then merged in
+  // wave order.
+  float pm[kSharedWaves], pd[kSharedWaves], pn[kSharedWaves];
+#pragma unroll
+  for (int w = 0; w < kSharedWaves; ++w) {
+    pm[w] = part_m[w];
+    pd[w] = part_den[w];
+    pn[w] = part_num[w][lane];
+  }
   float Mg = kNegInf;
 #pragma unroll
-  for (int w = 0; w < kSharedWaves; ++w) Mg = part_m[w] > Mg ? part_m[w] : Mg;
+  for (int w = 0; w < kSharedWaves; ++w) Mg = pm[w] > Mg ? pm[w] : Mg;
   float ng = 0.0f, dg = 0.0f;
   if (Mg > kNegInf) {
 #pragma unroll
     for (int w = 0; w < kSharedWaves; ++w) {
-      if (part_m[w] > kNegInf) {
-        const float a = __builtin_amdgcn_exp2f(part_m[w] - Mg);
-        ng = fmaf(a, part_num[w][lane], ng);
-        dg = fmaf(a, part_den[w], dg);
+      if (pm[w] > kNegInf) {
+        const float a = __builtin_amdgcn_exp2f(pm[w] - Mg);
+        ng = fmaf(a, pn[w], ng);
+        dg = fmaf(a, pd[w], dg);
       }
     }
   }
