@@ -414,6 +414,19 @@ __global__ __launch_bounds__(kSharedWaves * 64) void combine_shared(const Combin
   if (tok >= bound) return;  // padding row, uniform over the work-group
   const int S = c.seq_lens != nullptr ? splits_of_marker(c, bits) : c.num_splits;
   if (c.seq_lens != nullptr && S == 1) return;  // written to out by the attention kernel
+  if (S <= kSharedWaves * kSharedBlock && kSharedBlock * wave >= S) {
+    // No live split in this wave's block: an empty result, without waiting
+    // for the partial rows loaded speculatively (slots nobody wrote, often
+    // the slowest loads of the round).
+    if (lane == 0) {
+      part_m[wave] = kNegInf;
+      part_den[wave] = 0.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < NC; ++i) part_num[wave][i][lane] = 0.0f;
+    __syncthreads();
+    return;
+  }
   float M, den;
   float num[NC];
   if (S <= kSharedWaves * kSharedBlock)
