@@ -523,6 +523,10 @@ def measure_config(config: int, query_tokens: int, steps: int, warmup: int, cpu_
                           else "inputs exceed 1 GiB: read once per call")},
         "steps": steps, "warmup_steps_run": warm, "wall_s": round(wall, 3),
     }
+    if S == 1:
+        res["kernels_note"] = ("one launch per layer call (num_splits 1): kernels_us.attention and "
+                               "the layer call time the same kernel (interleaved-block medians against "
+                               "one timed loop); their difference is run-to-run noise")
     if is_prefill:
         tf = flops / (attn_ms * 1e-3) / 1e12
         res["roofline"] = {"bound": "mfma", "achieved": round(tf, 1), "peak": PEAK_BF16_TFLOPS,
